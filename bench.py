@@ -1,0 +1,441 @@
+"""Benchmark of the matrix-multiplication hot path on one MI355X.
+
+One step = one pass of the d_model-256 byte-LM training-step GEMM set
+(T = 4096 tokens, 5 layers x {forward, dX, dW} = 15 GEMMs, 20,937,965,568 FLOP)
+on the f16-in/f32-accumulate route, replayed from a HIP graph.  `value` is that
+set's TFLOP/s.  The same JSON line carries the other configurations measured in
+the same run (256^3 f32, the tape backward forms, the f32 step set, batched
+causal attention, the 125M-key 2-bit kNN scan), a roofline for the dominant
+kernel of each headline, and the CPU baseline (the oracle's restatement of the
+reference CPU path, one thread) on a bounded sample.
+
+    python bench.py [--steps K] [--warmup W] [--only gemm|knn|all] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOP/s + % MFMA peak at d_model-256 step shapes; kNN keys/s + % HBM BW"
+PEAK = {"f16": 2500.0, "f32": 157.3, "hbm_gbs": 8000.0}  # MI355X dense TFLOP/s, HBM GB/s
+T_TOKENS = 4096
+LAYERS = [("qkv", 256, 768), ("out", 256, 256), ("ffn1", 256, 1024), ("ffn2", 1024, 256), ("head", 256, 256)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+# --------------------------------------------------------------------------- timing helpers
+
+def time_events(fn, reps, stream):
+    """Average ms per call of fn() over `reps` calls, HIP events on `stream`."""
+    import torch
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(reps):
+        fn()
+    e.record(stream)
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def time_graph(fn, steps, warmup, stream):
+    """Captures fn() into a HIP graph; returns (ms per replay, graph)."""
+    import torch
+    fn()  # eager once more so every scratch buffer exists before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = time_events(g.replay, steps, stream)
+    return ms, g
+
+
+# --------------------------------------------------------------------------- GEMM step set
+
+class StepSet:
+    """Buffers and the 15 GEMM calls of one d=256 training step (f32 operands in HBM)."""
+
+    def __init__(self, dev, seed=1):
+        import torch
+        import oracle
+        self.calls = []
+        rng = oracle.Rng(seed)
+        T = T_TOKENS
+        self.bufs = []
+        for name, K, N in LAYERS:
+            X = torch.from_numpy(rng.gaussian(T * K)).to(dev)
+            W = torch.from_numpy(rng.gaussian(K * N, 0.02)).to(dev)
+            dY = torch.from_numpy(rng.gaussian(T * N)).to(dev)
+            Y, dX, dW = (torch.zeros(n, device=dev) for n in (T * N, T * K, K * N))
+            self.bufs.append((X, W, dY, Y, dX, dW))
+            # (label, a, b, out, m, k, n)
+            self.calls.append((f"{name} fwd", dict(h=X), dict(h=W), dict(h=Y), T, K, N))
+            self.calls.append((f"{name} dX", dict(h=dY), dict(h=W, trans=True), dict(h=dX), T, N, K))
+            self.calls.append((f"{name} dW", dict(h=X, trans=True), dict(h=dY), dict(h=dW), K, T, N))
+        self.flops = sum(2 * m * k * n for _, _, _, _, m, k, n in self.calls)
+        self.bytes = sum(4 * (m * k + k * n + m * n) for _, _, _, _, m, k, n in self.calls)
+
+    def call_fn(self, i, use_f16):
+        import scratchtape_amd as st
+        _, a, b, o, m, k, n = self.calls[i]
+        A, B, O = st.MatRef(**a), st.MatRef(**b), st.MatRef(**o)
+        return lambda: st.matmul_with(A, B, O, 1, m, k, n, None, use_f16)
+
+    def step_fn(self, use_f16):
+        fns = [self.call_fn(i, use_f16) for i in range(len(self.calls))]
+
+        def step():
+            for f in fns:
+                f()
+        return step
+
+
+def bench_gemm_set(dev, stream, steps, warmup, use_f16):
+    import torch
+    ss = StepSet(dev)
+    step = ss.step_fn(use_f16)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        eager_ms = time_events(step, steps, stream)
+        graph_ms, _ = time_graph(step, steps, warmup, stream)
+        per_call = []
+        for i, (label, _, _, _, m, k, n) in enumerate(ss.calls):
+            f = ss.call_fn(i, use_f16)
+            f()
+            ms = time_events(f, 50, stream)
+            fl = 2 * m * k * n
+            per_call.append(dict(gemm=label, m=m, k=k, n=n, ms=round(ms, 5), tflops=round(fl / ms / 1e9, 2),
+                                 gbs=round(4 * (m * k + k * n + m * n) / ms / 1e6, 1)))
+    torch.cuda.synchronize()
+    return ss, eager_ms, graph_ms, per_call
+
+
+def check_gemm_set(ss, use_f16, which=(2, 5, 8)):
+    """Parity of a few GEMMs of the timed set against the oracle (the bench refuses to report wrong numbers)."""
+    import oracle
+    errs = []
+    for i in which:
+        label, a, b, o, m, k, n = ss.calls[i]
+        A = a["h"].cpu().numpy()
+        B = b["h"].cpu().numpy()
+        A = A.reshape(k, m).T.copy() if a.get("trans") else A.reshape(m, k)
+        B = B.reshape(n, k).T.copy() if b.get("trans") else B.reshape(k, n)
+        r = oracle.round_f16 if use_f16 else (lambda x: x)
+        want = oracle.matmul(r(A), r(B))
+        got = o["h"].cpu().numpy().reshape(m, n)
+        errs.append(float(np.max(np.abs(got - want)) / np.max(np.abs(want))))
+    return max(errs)
+
+
+def cpu_gemm_baseline(ss):
+    """The reference CPU path (NdArray::matmul, with the explicit transposes the tape makes) on one full step set."""
+    import oracle
+    host = [(a["h"].cpu().numpy(), b["h"].cpu().numpy(), a.get("trans", False), b.get("trans", False), m, k, n)
+            for _, a, b, _, m, k, n in ss.calls]
+    t0 = time.perf_counter()
+    for A, B, ta, tb, m, k, n in host:
+        A2 = oracle.transpose(A.reshape(k, m)) if ta else A.reshape(m, k)
+        B2 = oracle.transpose(B.reshape(n, k)) if tb else B.reshape(k, n)
+        oracle.matmul(A2, B2)
+    dt = time.perf_counter() - t0
+    return dict(value=round(ss.flops / dt / 1e12, 5), unit="TFLOP/s", cores=1, kind="port",
+                sample="one full d=256 step GEMM set (15 GEMMs, 20.9 GFLOP) through the oracle's restatement of "
+                       "NdArray::matmul (tensor.rs:248-276) incl. the tape's explicit transposes, 1 thread, "
+                       f"gcc -O3 -mavx2 -mfma -ffp-contract=off, {cpu_model()}", seconds=round(dt, 3))
+
+
+# --------------------------------------------------------------------------- smaller GEMM configs
+
+def bench_tape_forms(dev, stream, m, k, n, use_f16, reps=50):
+    """C = A·B, dA = dC·Bᵀ, dB = Aᵀ·dC with A [m,k], B [k,n], dC [m,n] uniform [-1,1] (seeded)."""
+    import torch
+    import oracle
+    import scratchtape_amd as st
+    rng = oracle.Rng(42)
+    A, B, dC = (torch.from_numpy(rng.uniform(x)).to(dev) for x in (m * k, k * n, m * n))
+    C, dA, dB = (torch.zeros(x, device=dev) for x in (m * n, m * k, k * n))
+    forms = {
+        "C=A·B": (lambda: st.matmul_with(st.MatRef(A), st.MatRef(B), st.MatRef(C), 1, m, k, n, None, use_f16), m, k, n),
+        "dA=dC·Bᵀ": (lambda: st.matmul_with(st.MatRef(dC), st.MatRef(B, trans=True), st.MatRef(dA), 1, m, n, k, None,
+                                             use_f16), m, n, k),
+        "dB=Aᵀ·dC": (lambda: st.matmul_with(st.MatRef(A, trans=True), st.MatRef(dC), st.MatRef(dB), 1, k, m, n, None,
+                                             use_f16), k, m, n),
+    }
+    out = {}
+    with torch.cuda.stream(stream):
+        for name, (f, mm, kk, nn) in forms.items():
+            f()
+            ms = time_events(f, reps, stream)
+            out[name] = dict(m=mm, k=kk, n=nn, ms=round(ms, 5), tflops=round(2 * mm * kk * nn / ms / 1e9, 3))
+    return out
+
+
+# --------------------------------------------------------------------------- attention
+
+def bench_attention(dev, stream, steps, warmup, use_f16):
+    import torch
+    import oracle
+    from scratchtape_amd import attention
+    b, h, t, hd = 32, 4, 128, 64
+    d = h * hd
+    rng = oracle.Rng(17)
+    qkv = rng.gaussian(b * t * 3 * d)
+    if use_f16:
+        qkv = oracle.round_f16(qkv)
+    qkv = torch.from_numpy(qkv).to(dev)
+    dctx = torch.from_numpy(rng.gaussian(b * t * d)).to(dev)
+    buf = attention.AttnBuffers.empty(b, h, t, hd, dev)
+    step = lambda: attention.step(qkv, dctx, buf, b, h, t, hd, use_f16)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        eager_ms = time_events(step, steps, stream)
+        graph_ms, _ = time_graph(step, steps, warmup, stream)
+    flops = 6 * b * h * 2 * t * t * hd
+    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_ms=round(graph_ms, 5),
+                tflops=round(flops / graph_ms / 1e9, 3))
+
+
+def cpu_attention_baseline():
+    import oracle
+    b, h, t, hd = 32, 4, 128, 64
+    rng = oracle.Rng(3)
+    q, k, v, do = (rng.gaussian(b * h * t * hd) for _ in range(4))
+    t0 = time.perf_counter()
+    oracle.attention_fwd_bwd(q, k, v, do, b * h, t, hd, hd ** -0.5)
+    dt = time.perf_counter() - t0
+    flops = 6 * b * h * 2 * t * t * hd
+    return dict(value=round(flops / dt / 1e12, 5), unit="TFLOP/s", cores=1, kind="port", seconds=round(dt, 3),
+                sample="one full attention fwd+bwd (128 chunks of 128x128x64) through the per-chunk loop of "
+                       "tape.rs:73-112 restated in the oracle, 1 thread")
+
+
+# --------------------------------------------------------------------------- kNN
+
+class KnnBench:
+    N, NCELLS, NQ, NPROBE, D = 125_000_000, 12288, 256, 8, 256
+
+    def __init__(self, dev, batches=8, seed=2024):
+        import torch
+        from scratchtape_amd import knn
+        rng = np.random.default_rng(seed)
+        sizes = rng.multinomial(self.N, np.full(self.NCELLS, 1.0 / self.NCELLS))
+        self.cs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+        self.codes = torch.empty((self.N, self.D // 4), dtype=torch.uint8, device=dev)
+        self.scales = torch.empty(self.N, dtype=torch.float32, device=dev)
+        t0 = time.perf_counter()
+        knn.synth_store_2bit(seed, 0, self.codes, self.scales)
+        torch.cuda.synchronize()
+        self.gen_s = time.perf_counter() - t0
+        self.store = knn.KnnStore2bit(self.codes, self.scales, self.cs)
+        self.batches = []
+        for _ in range(batches):
+            q = rng.standard_normal((self.NQ, self.D)).astype(np.float32)
+            p = np.stack([rng.choice(self.NCELLS, self.NPROBE, replace=False) for _ in range(self.NQ)]).astype(np.int32)
+            pairs = int(sizes[p].sum())
+            distinct = np.unique(p)
+            dbytes = int(sizes[distinct].sum()) * (self.D // 4 + 4)
+            self.batches.append(dict(q=torch.from_numpy(q).to(dev), p=torch.from_numpy(p).to(dev), qh=q, ph=p,
+                                     pairs=pairs, bytes=dbytes))
+        self.out = (torch.empty((self.NQ, 128), dtype=torch.int64, device=dev),
+                    torch.empty((self.NQ, 128), dtype=torch.float32, device=dev))
+
+    def search(self, i):
+        bt = self.batches[i % len(self.batches)]
+        return self.store.search_ivf(bt["q"], bt["p"], 128, out=self.out)
+
+    def run(self, stream, steps, warmup):
+        import torch
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                self.search(i)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for i in range(steps):
+                self.search(i)
+            e.record(stream)
+            e.synchronize()
+            ms = s.elapsed_time(e) / steps
+        nb = len(self.batches)
+        pairs = np.mean([self.batches[i % nb]["pairs"] for i in range(steps)])
+        byts = np.mean([self.batches[i % nb]["bytes"] for i in range(steps)])
+        return ms, pairs, byts
+
+    def check(self, qis=(0, 100, 255)):
+        """Bit-exact top-128 for a few queries of batch 0 against the oracle over the same stored bytes."""
+        import torch
+        import oracle
+        idx, dist = self.search(0)
+        idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+        bt = self.batches[0]
+        for qi in qis:
+            cells = bt["ph"][qi]
+            rows = np.concatenate([np.arange(self.cs[c], self.cs[c + 1]) for c in cells])
+            sub = np.concatenate([[0], np.cumsum([self.cs[c + 1] - self.cs[c] for c in cells])]).astype(np.int64)
+            sel = torch.from_numpy(rows).to(self.codes.device)
+            widx, wdist = oracle.knn_search(self.codes[sel].cpu().numpy(), self.scales[sel].cpu().numpy(), sub,
+                                            bt["qh"][qi:qi + 1], np.arange(len(cells), dtype=np.int32)[None], 128)
+            if not (np.array_equal(idx[qi], rows[widx[0]]) and np.array_equal(dist[qi], wdist[0])):
+                return False
+        return True
+
+    def cpu_baseline(self, nq=24):
+        """The oracle's exact 2-bit scoring + top-128 over the same probed cells, 1 thread."""
+        import torch
+        import oracle
+        bt = self.batches[1]
+        total_pairs, dt = 0, 0.0
+        for qi in range(nq):
+            cells = bt["ph"][qi]
+            rows = np.concatenate([np.arange(self.cs[c], self.cs[c + 1]) for c in cells])
+            sub = np.concatenate([[0], np.cumsum([self.cs[c + 1] - self.cs[c] for c in cells])]).astype(np.int64)
+            sel = torch.from_numpy(rows).to(self.codes.device)
+            codes, scales = self.codes[sel].cpu().numpy(), self.scales[sel].cpu().numpy()
+            t0 = time.perf_counter()
+            oracle.knn_search(codes, scales, sub, bt["qh"][qi:qi + 1], np.arange(len(cells), dtype=np.int32)[None], 128)
+            dt += time.perf_counter() - t0
+            total_pairs += rows.size
+        return dict(value=round(total_pairs / dt / 1e9, 5), unit="G keys/s", cores=1, kind="port",
+                    seconds=round(dt, 3),
+                    sample=f"{nq} queries x 8 probed cells of the 125M-key store ({total_pairs} pairs), exact 2-bit "
+                           "scoring + top-128 by (score, index) in the oracle (C, 1 thread); the reference has no "
+                           "CPU quantised scorer")
+
+
+# --------------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["all", "gemm", "knn"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X (asked for --gpus {args.gpus}); "
+              "see the sharding design for more than one", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import scratchtape_amd as st
+    st.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.init()
+    stream = torch.cuda.Stream(device=dev)
+    prop = torch.cuda.get_device_properties(dev)
+    extra = {"device": prop.name, "cus": prop.multi_processor_count, "host_cpu": cpu_model(), "nproc": os.cpu_count()}
+    result = None
+
+    if args.only in ("all", "gemm"):
+        log("[bench] C3 step GEMM set, f16-in/f32-acc")
+        ss16, eager16, graph16, calls16 = bench_gemm_set(dev, stream, args.steps, args.warmup, True)
+        err16 = check_gemm_set(ss16, True)
+        log(f"[bench] f16 set: graph {graph16:.4f} ms, eager {eager16:.4f} ms, parity {err16:.2e}")
+        log("[bench] C3 step GEMM set, f32")
+        ss32, eager32, graph32, calls32 = bench_gemm_set(dev, stream, args.steps, args.warmup, False)
+        err32 = check_gemm_set(ss32, False)
+        log(f"[bench] f32 set: graph {graph32:.4f} ms, eager {eager32:.4f} ms, parity {err32:.2e}")
+        if err16 > 1e-5 or err32 > 1e-5:
+            log("[bench] PARITY FAILURE: refusing to report")
+            sys.exit(3)
+        dom = max(calls16, key=lambda c: c["ms"])
+        value = ss16.flops / graph16 / 1e9
+        roof = dict(kernel=f"k_gemm f16 ({dom['gemm']}: {dom['m']}x{dom['k']}x{dom['n']})", bound="mfma",
+                    achieved=dom["tflops"], peak=PEAK["f16"], unit="TFLOP/s",
+                    frac=round(dom["tflops"] / PEAK["f16"], 4), traffic=None,
+                    hbm_gbs=dom["gbs"], hbm_frac=round(dom["gbs"] / PEAK["hbm_gbs"], 4))
+        extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes, graph_ms=round(graph16, 5),
+                                   eager_ms=round(eager16, 5), tflops=round(value, 2),
+                                   mfma_frac=round(value / PEAK["f16"], 4),
+                                   hbm_gbs=round(ss16.bytes / graph16 / 1e6, 1), per_gemm=calls16,
+                                   parity_max_rel_err=err16)
+        v32 = ss32.flops / graph32 / 1e9
+        extra["c3_f32_set"] = dict(graph_ms=round(graph32, 5), eager_ms=round(eager32, 5), tflops=round(v32, 2),
+                                   mfma_frac=round(v32 / PEAK["f32"], 4), per_gemm=calls32, parity_max_rel_err=err32)
+        log("[bench] C1 / C2 tape forms")
+        extra["c1_256cube_f32"] = bench_tape_forms(dev, stream, 256, 256, 256, False)
+        extra["c2_backward_f32"] = bench_tape_forms(dev, stream, 4096, 256, 1024, False)
+        extra["c2_backward_f16"] = bench_tape_forms(dev, stream, 4096, 256, 1024, True)
+        log("[bench] C4 attention")
+        extra["c4_attention_f16"] = bench_attention(dev, stream, args.steps, args.warmup, True)
+        extra["c4_attention_f32"] = bench_attention(dev, stream, args.steps, args.warmup, False)
+        cpu = None
+        if not args.no_cpu:
+            log("[bench] CPU baselines (oracle, 1 thread)")
+            cpu = cpu_gemm_baseline(ss16)
+            extra["c4_attention_cpu_baseline"] = cpu_attention_baseline()
+        result = dict(metric=METRIC, value=round(value, 3), unit="TFLOP/s", n_gpus=1, steps=args.steps,
+                      warmup=args.warmup, ms_per_step=round(graph16, 5), higher_is_better=True, scaling="weak",
+                      vs_baseline=None, dtype="f16-in/f32-acc",
+                      data="synthetic (seeded nn::Rng restatement: weights N(0,0.02), activations N(0,1))",
+                      config=dict(workload="d_model-256 training-step GEMM set: T=4096 tokens, QKV/out/FFN1/FFN2/"
+                                           "head forward + dX + dW (15 GEMMs), f32 operands in HBM, f16-in/f32-acc",
+                                  global_batch=T_TOKENS, seq_len=128, parallelism="none (1 GPU)"),
+                      roofline=roof, cpu_baseline=cpu)
+        del ss16, ss32
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "knn"):
+        log("[bench] C5 kNN store (125M 2-bit keys)")
+        kb = KnnBench(dev)
+        ok = kb.check()
+        log(f"[bench] kNN store generated in {kb.gen_s:.2f} s; parity {'ok' if ok else 'FAILED'}")
+        if not ok:
+            log("[bench] PARITY FAILURE: refusing to report")
+            sys.exit(3)
+        ms, pairs, byts = kb.run(stream, args.steps, args.warmup)
+        gbs = byts / ms / 1e6
+        knn = dict(ms_per_batch=round(ms, 5), keys_per_s=round(pairs / ms * 1e3, 1),
+                   g_keys_per_s=round(pairs / ms / 1e6, 3), pairs_per_batch=int(pairs),
+                   distinct_cell_bytes=int(byts), hbm_gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK["hbm_gbs"], 4),
+                   roofline=dict(kernel="st_knn_search_ivf_2bit (k_prep + k_scan + k_merge)", bound="hbm",
+                                 achieved=round(gbs, 1), peak=PEAK["hbm_gbs"], unit="GB/s",
+                                 frac=round(gbs / PEAK["hbm_gbs"], 4), traffic=None),
+                   store_gen_s=round(kb.gen_s, 3))
+        if not args.no_cpu:
+            knn["cpu_baseline"] = kb.cpu_baseline()
+        extra["c5_knn"] = knn
+        if result is None:
+            result = dict(metric=METRIC, value=knn["g_keys_per_s"], unit="G keys/s", n_gpus=1, steps=args.steps,
+                          warmup=args.warmup, ms_per_step=knn["ms_per_batch"], higher_is_better=True,
+                          scaling="weak", vs_baseline=None, dtype="u8 codes / int32 dot",
+                          data="synthetic (counter-based N(0,1) keys, seeded queries and probes)",
+                          config=dict(workload="125M 2-bit keys, 12288 cells, 256 queries x 8 probes, top-128"),
+                          roofline=knn["roofline"], cpu_baseline=knn.get("cpu_baseline"))
+        del kb
+        torch.cuda.empty_cache()
+
+    result["extra"] = extra
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/*
+ * scratchtape_hip.h — C ABI of the MI355X (gfx950) matrix-multiplication hot
+ * path of scratchtape.  Every entry point is a drop-in for one reference
+ * interface (cited per declaration, paths relative to the reference crate).
+ *
+ * Conventions
+ *  - Device buffers are plain device pointers (the reference's cubecl
+ *    `Handle`s).  The caller owns every operand and output; outputs are
+ *    written in place.  The library owns only a grow-only scratch arena per
+ *    device (split-k partials, kNN candidate lists), like the reference's
+ *    `split_scratch` (gpu_step/matmul.rs:207-217) and `KnnStore::scratch`
+ *    (gpu_step/knn.rs:74-105).
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL is the default
+ *    stream) and is asynchronous, as the reference's single in-order queue
+ *    (gpu_step/mod.rs:42, 78).  Calls that use the scratch arena (split-k
+ *    GEMMs, kNN search) must be serialised on one stream per device.
+ *  - The reference panics (assert!/expect) on bad arguments.  Panics cannot
+ *    cross an FFI boundary, so every entry point returns an st_status and
+ *    st_last_error() gives the message (thread-local), whose text follows
+ *    the reference's assert messages where one exists.
+ */
+#ifndef SCRATCHTAPE_HIP_H
+#define SCRATCHTAPE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t st_status;
+#define ST_OK 0
+#define ST_ERR_INVALID (-1)     /* bad shape or argument (the reference's assert) */
+#define ST_ERR_HIP (-2)         /* a HIP runtime call failed */
+#define ST_ERR_OOM (-3)         /* scratch arena could not grow */
+#define ST_ERR_NO_DEVICE (-4)   /* no gfx950 device visible */
+
+typedef void *st_stream; /* hipStream_t */
+
+/* A matrix inside a device buffer: gpu_step/matmul.rs:26-60 `MatRef`.
+ * Matrix z starts at p + off + (z / group)*stride + (z % group)*inner; its
+ * stored rows are `ld` apart (0: packed, the stored row length); `trans`: a
+ * logical [r, c] operand stored as [c, r].  group 0 is read as 1. */
+typedef struct st_matref {
+    float *p;
+    int64_t off;
+    int64_t stride;
+    int32_t trans;
+    int32_t reserved;
+    int64_t ld;
+    int64_t group;
+    int64_t inner;
+} st_matref;
+
+/* gpu_step/matmul.rs:62-79 `Epilogue`, applied in this order per output
+ * element: + bias[bias_off + z*bias_stride + col], ReLU, zero where
+ * mask[mask_off + (element index in out's layout)] <= 0, + residual (same
+ * layout as out), + the value already in out (accumulate).  col_sum: also
+ * add the column sums of b[z] over k into out.p[col_sum_off + z*col_sum_stride
+ * + j] (always +=), summed in a fixed order.  NULL pointers mean "absent". */
+typedef struct st_epilogue {
+    const float *bias;
+    int64_t bias_off;
+    int64_t bias_stride;
+    const float *mask;
+    int64_t mask_off;
+    const float *residual;
+    int64_t residual_off;
+    int32_t relu;
+    int32_t accumulate;
+    int32_t has_col_sum;
+    int32_t reserved;
+    int64_t col_sum_off;
+    int64_t col_sum_stride;
+} st_epilogue;
+
+/* ---- GEMM: the three tape forms, batched, head views, epilogue ---------- */
+
+/* gpu_step/matmul.rs:86 `matmul`: out[z] (+)= epi(a[z] @ b[z]) for z in
+ * 0..batch, a[z] logically [m, k], b[z] [k, n], out row-major [m, n]
+ * (out->trans must be 0: "out is stored row-major", matmul.rs:107).  Runs
+ * f16-in/f32-accumulate when st_f16_enabled() and the shape tiles
+ * (k % 32 == 0, m % 64 == 0, n % 32 == 0, and not col_sum with b
+ * transposed: matmul.rs:108-112, 524-534), else f32.  epi may be NULL. */
+st_status st_matmul(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch,
+                    int64_t m, int64_t k, int64_t n, const st_epilogue *epi, st_stream stream);
+
+/* gpu_step/matmul.rs:93 `matmul_f32`: the same, always f32 (the reference's
+ * attention matmuls). */
+st_status st_matmul_f32(const st_matref *a, const st_matref *b, const st_matref *out,
+                        int64_t batch, int64_t m, int64_t k, int64_t n, const st_epilogue *epi,
+                        st_stream stream);
+
+/* gpu_step/matmul.rs:106 `matmul_with`: the f16 route chosen by the caller
+ * (it still falls back to f32 for shapes it cannot tile). */
+st_status st_matmul_with(const st_matref *a, const st_matref *b, const st_matref *out,
+                         int64_t batch, int64_t m, int64_t k, int64_t n, const st_epilogue *epi,
+                         int32_t use_f16, st_stream stream);
+
+/* gpu_step/matmul.rs:97-102 `f16_enabled`: 1 unless the environment sets
+ * TRAIN_F16=0 (gfx950 always has f16 x f16 -> f32 matrix cores).  Read once. */
+int32_t st_f16_enabled(void);
+
+/* src/tensor.rs:241 `NdArray::matmul` on host buffers: out[m, n] = a[m, k] @
+ * b[k, n], row-major f32, computed on the GPU in f32 (host buffers in and out;
+ * synchronous).  Thread-safe. */
+st_status st_ndarray_matmul(const float *a, const float *b, float *out, int64_t m, int64_t k,
+                            int64_t n);
+
+/* ---- Row kernels of the attention configuration ------------------------ */
+
+/* gpu_step/rows.rs:101-112 `softmax`: y = softmax(scale * x) per row of
+ * x [rows, n].  causal: row r sees columns 0..=r % t, the rest are exactly
+ * 0.  one: softmax1 (phantom logit 0, shift max(row max, 0)). */
+st_status st_softmax(const float *x, float *y, int64_t rows, int64_t n, int64_t t, float scale,
+                     int32_t causal, int32_t one, st_stream stream);
+
+/* gpu_step/rows.rs:114-123 `softmax_backward`: dx = scale * y * (dy - sum(dy*y)). */
+st_status st_softmax_backward(const float *dy, const float *y, float *dx, int64_t rows, int64_t n,
+                              float scale, st_stream stream);
+
+/* ---- 2-bit kNN memory ---------------------------------------------------- */
+
+/* gpu_step/knn.rs:190-225 `tile_of` (bits = 2) on the device: keys [n, d]
+ * f32 -> codes [n, d/4] (code i at byte i/4, bits 2(i%4)) and one f32 scale
+ * per key, bit-identical to the reference's host quantiser.  d % 16 == 0. */
+st_status st_knn_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t *codes,
+                               float *scales, st_stream stream);
+
+/* gpu_step/knn/ivf.rs:466 `KnnStore::search_ivf`, the scored part
+ * (scan_group ivf.rs:528-686: fused dequant-dot, top-k, merge, finalise),
+ * given each query's probed cells.  The store holds keys cell-contiguous:
+ * cell c is rows cell_start[c]..cell_start[c+1] of codes [N, d/4] and
+ * scales [N]; max_cell is the largest cell's row count (host-known from the
+ * store build).  queries [nq, d] f32, probes [nq, nprobe] int32 cell ids (a
+ * cell repeated within one query's probes is scanned once).  Outputs, per
+ * query, the k (<= 128, KMAX knn.rs:21) nearest by the exact 2-bit score,
+ * ascending by (distance, key index): out_idx [nq, k] global rows (-1
+ * padding), out_dist [nq, k] = max(|q^|^2 + dist, 0) (+inf padding).
+ * All pointers are device pointers; d == 256. */
+st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *scales,
+                                 const int64_t *cell_start, int64_t ncells, int64_t max_cell,
+                                 const float *queries, const int32_t *probes, int64_t nq,
+                                 int64_t nprobe, int64_t d, int64_t k, int64_t *out_idx,
+                                 float *out_dist, st_stream stream);
+
+/* Benchmark support, no reference counterpart: fills rows [row0, row0 + n)
+ * of a synthetic 2-bit store with keys drawn N(0,1) from a counter-based
+ * generator (seed, global row, component) and quantised as
+ * st_knn_quantize_2bit, without materialising the f32 keys.  d == 256. */
+st_status st_knn_synth_store_2bit(uint64_t seed, int64_t row0, int64_t n, int64_t d,
+                                  uint8_t *codes, float *scales, st_stream stream);
+
+/* Benchmark/test support, no reference counterpart: the f32 keys [n, d] that
+ * st_knn_synth_store_2bit quantises for rows [row0, row0 + n). */
+st_status st_knn_synth_keys_f32(uint64_t seed, int64_t row0, int64_t n, int64_t d, float *keys,
+                                st_stream stream);
+
+/* ---- Misc ---------------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *st_last_error(void);
+
+/* Waits for the work enqueued on `stream`. */
+st_status st_sync(st_stream stream);
+
+/* Library version string. */
+const char *st_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCRATCHTAPE_HIP_H */

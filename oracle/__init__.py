@@ -1,0 +1,274 @@
+"""CPU oracle for the scratchtape matrix-multiplication hot path.
+
+TEST INFRASTRUCTURE ONLY: the checker used by ``tests/``, by the package
+``__graft_entry__.smoke()`` and by ``bench.py``'s CPU baseline.  The product
+library (``scratchtape_amd``) never imports this module.
+
+The arithmetic lives in ``oracle.c`` (built to ``liboracle.so`` by the Makefile
+beside it); this module only wraps it with numpy.  Each function names the
+reference code it restates and how it is pinned (the test that pins it):
+
+=====================  =========================================  ======================================================
+function               reference                                  pinned by (tests/test_oracle.py)
+=====================  =========================================  ======================================================
+Rng                    src/nn.rs:8-35 (xorshift64 13/7/17)        Marsaglia's published xorshift64 outputs; big-int
+                                                                   recurrence; next_f32 range; Box-Muller moments
+matmul                 src/tensor.rs:241-276                      gpu.rs:176-185 KAT; integer-valued inputs vs exact
+                                                                   int64 products; identity/permutation; float64 bound;
+                                                                   bit-equality with an independent p-ascending
+                                                                   float32 accumulation and inequality with FMA order
+transpose              src/tensor.rs:278-287                      involution, numpy .T
+round_f16              half 2.7.1 from_f32 (RNE)                  IEEE-754 tie/overflow/subnormal KATs; numpy float16
+gemm (MatRef/Epilogue)  gpu_step/matmul.rs:26-79, 888-937         integer-valued exactness vs numpy int64 per epilogue
+                                                                   term; head views vs explicit split_heads slicing
+softmax / backward     gpu_step/rows.rs:101-123, 295-357          float64 softmax; rows sum to 1; masked entries exactly
+                                                                   0; finite-difference gradient; softmax1 phantom term
+attention_fwd_bwd      src/tape.rs:73-112 (+ causal mask)         float64 closed-form attention forward and gradients
+quantize_2bit          gpu_step/knn.rs:190-225 (bits 2)           hand-computed rows (ties round away from zero, clamp,
+                                                                   packing order, 1e-30 floor); float64 scale formula
+knn_prep_query         build contract (int16 query)               exactness: Q*qs reproduces q to half an ulp of qs;
+                                                                   power-of-two qs; |Q| range
+knn_search             build contract (ivf.rs:235 distance,       int64 brute force + numpy float32 formula + lexsort;
+                       ivf.rs:673-684 finalisation)               exact integer dot vs float64; fidelity to the
+                                                                   reference's own f16 scoring within its 2e-3 tolerance
+=====================  =========================================  ======================================================
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_i16p = np.ctypeslib.ndpointer(dtype=np.int16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_u64 = ctypes.c_uint64
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+
+class _MatRef(ctypes.Structure):
+    _fields_ = [("off", _i64), ("stride", _i64), ("trans", _i64), ("ld", _i64), ("group", _i64), ("inner", _i64)]
+
+
+class QPrep(ctypes.Structure):
+    _fields_ = [("qs", ctypes.c_float), ("qn", ctypes.c_float), ("sq", _i32), ("pad", _i32)]
+
+
+def build() -> None:
+    """Compile liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_rng_next_f32.argtypes = [ctypes.POINTER(_u64)]
+        L.orc_rng_next_f32.restype = ctypes.c_float
+        L.orc_rng_next_gaussian.argtypes = [ctypes.POINTER(_u64)]
+        L.orc_rng_next_gaussian.restype = ctypes.c_float
+        L.orc_rng_fill_uniform.argtypes = [ctypes.POINTER(_u64), _i64, _f32p]
+        L.orc_rng_fill_gaussian.argtypes = [ctypes.POINTER(_u64), _i64, ctypes.c_float, _f32p]
+        L.orc_matmul.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64]
+        L.orc_transpose.argtypes = [_f32p, _f32p, _i64, _i64]
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_round_f16_array.argtypes = [_f32p, _f32p, _i64]
+        L.orc_gemm.argtypes = [
+            _f32p, ctypes.POINTER(_MatRef), _f32p, ctypes.POINTER(_MatRef), _f32p, ctypes.POINTER(_MatRef),
+            _i64, _i64, _i64, _i64,
+            ctypes.c_void_p, _i64, _i32, ctypes.c_void_p, ctypes.c_void_p, _i32, _i32, _i64, _i64, _i32,
+        ]
+        L.orc_softmax.argtypes = [_f32p, _f32p, _i64, _i64, _i64, ctypes.c_float, _i32, _i32]
+        L.orc_softmax_backward.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_float]
+        L.orc_attention_fwd_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_float,
+                                            _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_quantize_2bit.argtypes = [_f32p, _i64, _i64, _u8p, _f32p, ctypes.c_void_p]
+        L.orc_knn_prep_query.argtypes = [_f32p, _i64, _i16p, ctypes.POINTER(QPrep)]
+        L.orc_knn_dists.argtypes = [_u8p, _f32p, _i64, _i64, _i64, _i16p, ctypes.POINTER(QPrep), _f32p]
+        L.orc_knn_search.argtypes = [_u8p, _f32p, _i64p, _f32p, _i32p, _i64, _i64, _i64, _i64, _i64p, _f32p]
+        L.orc_knn_ref_f16_dist.argtypes = [_u8p, ctypes.c_float, ctypes.c_float, _f32p, _i64]
+        L.orc_knn_ref_f16_dist.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+# --------------------------------------------------------------------------- Rng (nn.rs:8-35)
+
+class Rng:
+    """xorshift64 state with the reference's next_f32 / next_gaussian."""
+
+    def __init__(self, seed: int):
+        self.state = _u64(seed)
+
+    def next_f32(self) -> float:
+        return lib().orc_rng_next_f32(ctypes.byref(self.state))
+
+    def next_gaussian(self) -> float:
+        return lib().orc_rng_next_gaussian(ctypes.byref(self.state))
+
+    def uniform(self, n: int) -> np.ndarray:
+        """n values of next_f32()*2-1 (gpu.rs:189-192)."""
+        out = np.empty(n, np.float32)
+        lib().orc_rng_fill_uniform(ctypes.byref(self.state), n, out)
+        return out
+
+    def gaussian(self, n: int, scale: float = 1.0) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        lib().orc_rng_fill_gaussian(ctypes.byref(self.state), n, scale, out)
+        return out
+
+
+# --------------------------------------------------------------------------- tensor.rs
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """NdArray::matmul (tensor.rs:241-276), bit-exact restatement."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    assert a.ndim == 2 and b.ndim == 2, "matmul is 2D only"
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2, f"matmul inner dims must match: {a.shape} vs {b.shape}"
+    out = np.empty((m, n), np.float32)
+    lib().orc_matmul(a, b, out, m, k, n)
+    return out
+
+
+def transpose(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    m, n = a.shape
+    out = np.empty((n, m), np.float32)
+    lib().orc_transpose(a, out, m, n)
+    return out
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_round_f16_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().orc_f32_to_f16(float(x)))
+
+
+# --------------------------------------------------------------------------- gpu_step::matmul semantics
+
+def _ref(off=0, stride=0, trans=False, ld=0, group=1, inner=0) -> _MatRef:
+    return _MatRef(off, stride, int(bool(trans)), ld, group, inner)
+
+
+def gemm(a_buf, a, b_buf, b, out_buf, out, batch, m, k, n, *, bias=None, bias_stride=0, relu=False,
+         mask=None, residual=None, accumulate=False, col_sum=None, f16=False):
+    """gpu_step::matmul's meaning (matmul.rs:62-106) on host buffers, in place on out_buf.
+
+    a, b, out are dicts with MatRef fields (off, stride, trans, ld, group, inner);
+    bias/mask/residual are (buffer, offset) pairs; col_sum is (offset, stride) into out_buf.
+    """
+    a_buf = np.ascontiguousarray(a_buf, np.float32)
+    b_buf = np.ascontiguousarray(b_buf, np.float32)
+    assert out_buf.dtype == np.float32 and out_buf.flags.c_contiguous
+    keep = []
+
+    def ptr(pair):
+        if pair is None:
+            return None
+        buf, off = pair
+        buf = np.ascontiguousarray(buf, np.float32)
+        keep.append(buf)
+        return buf.ctypes.data + 4 * off
+
+    cs_off, cs_stride = col_sum if col_sum is not None else (0, 0)
+    lib().orc_gemm(a_buf, ctypes.byref(_ref(**a)), b_buf, ctypes.byref(_ref(**b)), out_buf,
+                   ctypes.byref(_ref(**out)), batch, m, k, n, ptr(bias), bias_stride, int(relu),
+                   ptr(mask), ptr(residual), int(accumulate), int(col_sum is not None), cs_off, cs_stride,
+                   int(f16))
+    return out_buf
+
+
+# --------------------------------------------------------------------------- rows.rs
+
+def softmax(x: np.ndarray, rows: int, n: int, t: int, scale: float, causal: bool, one: bool) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    y = np.empty(rows * n, np.float32)
+    lib().orc_softmax(x, y, rows, n, t, scale, int(causal), int(one))
+    return y
+
+
+def softmax_backward(dy: np.ndarray, y: np.ndarray, rows: int, n: int, scale: float) -> np.ndarray:
+    dy = np.ascontiguousarray(dy, np.float32).reshape(-1)
+    y = np.ascontiguousarray(y, np.float32).reshape(-1)
+    dx = np.empty(rows * n, np.float32)
+    lib().orc_softmax_backward(dy, y, dx, rows, n, scale)
+    return dx
+
+
+def attention_fwd_bwd(q, k, v, dout, chunks, t, hd, scale):
+    """Per-chunk CPU attention forward + backward (tape.rs:73-112): returns P, O, dQ, dK, dV."""
+    arrs = [np.ascontiguousarray(x, np.float32).reshape(-1) for x in (q, k, v, dout)]
+    p = np.empty(chunks * t * t, np.float32)
+    o, dq, dk, dv = (np.empty(chunks * t * hd, np.float32) for _ in range(4))
+    scratch = np.empty(4 * t * t + 3 * t * hd, np.float32)
+    lib().orc_attention_fwd_bwd(*arrs, chunks, t, hd, scale, p, o, dq, dk, dv, scratch)
+    return p, o, dq, dk, dv
+
+
+# --------------------------------------------------------------------------- kNN (knn.rs, ivf.rs)
+
+def quantize_2bit(keys: np.ndarray, d: int, with_norm: bool = False):
+    """tile_of for 2-bit keys (knn.rs:190-225): codes [n, d/4] u8, scales [n] f32 (+ the f16 norms)."""
+    keys = np.ascontiguousarray(keys, np.float32).reshape(-1)
+    n = keys.size // d
+    codes = np.empty((n, d // 4), np.uint8)
+    scales = np.empty(n, np.float32)
+    norm = np.empty(n, np.float32) if with_norm else None
+    lib().orc_quantize_2bit(keys, n, d, codes, scales, norm.ctypes.data if with_norm else None)
+    return (codes, scales, norm) if with_norm else (codes, scales)
+
+
+def knn_prep_query(q: np.ndarray):
+    q = np.ascontiguousarray(q, np.float32).reshape(-1)
+    Q = np.empty(q.size, np.int16)
+    prep = QPrep()
+    lib().orc_knn_prep_query(q, q.size, Q, ctypes.byref(prep))
+    return Q, prep
+
+
+def knn_dists(codes, scales, d, r0, r1, q):
+    Q, prep = knn_prep_query(q)
+    out = np.empty(r1 - r0, np.float32)
+    lib().orc_knn_dists(np.ascontiguousarray(codes).reshape(-1), np.ascontiguousarray(scales), d, r0, r1, Q,
+                        ctypes.byref(prep), out)
+    return out
+
+
+def knn_search(codes, scales, cell_start, queries, probes, k=128):
+    """Top-k by (dist, key index) over each query's probed cells; returns (idx int64 [nq,k], dist f32 [nq,k])."""
+    codes = np.ascontiguousarray(codes, np.uint8).reshape(-1)
+    scales = np.ascontiguousarray(scales, np.float32)
+    cell_start = np.ascontiguousarray(cell_start, np.int64)
+    probes = np.ascontiguousarray(probes, np.int32)
+    nq, nprobe = probes.shape
+    d = (codes.size // scales.size) * 4
+    queries = np.ascontiguousarray(queries, np.float32).reshape(nq, d)
+    idx = np.empty((nq, k), np.int64)
+    dist = np.empty((nq, k), np.float32)
+    lib().orc_knn_search(codes, scales, cell_start, queries.reshape(-1), probes, nq, nprobe, d, k, idx, dist)
+    return idx, dist
+
+
+def knn_ref_f16_dist(code_row, scale, norm_f16, q):
+    return lib().orc_knn_ref_f16_dist(np.ascontiguousarray(code_row, np.uint8), float(scale), float(norm_f16),
+                                      np.ascontiguousarray(q, np.float32), q.size)

@@ -1,0 +1,16 @@
+"""scratchtape_amd: scratchtape's matrix-multiplication hot path on MI355X (gfx950).
+
+Hand-written HIP kernels behind the C ABI of include/scratchtape_hip.h
+(libscratchtape_hip.so, built in-tree by scratchtape_amd.build), with thin
+Python mirrors of the reference interfaces they replace:
+
+- matmul.MatRef / Epilogue / matmul / matmul_f32 / matmul_with  (gpu_step/matmul.rs)
+- tensor.ndarray_matmul                                         (src/tensor.rs NdArray::matmul)
+- rows.softmax / softmax_backward                               (gpu_step/rows.rs)
+- knn.KnnStore2bit / quantize_2bit                              (gpu_step/knn.rs, knn/ivf.rs)
+"""
+from ._lib import ScratchtapeError, lib  # noqa: F401
+from .matmul import Epilogue, MatRef, f16_enabled, f16_route, matmul, matmul_f32, matmul_with  # noqa: F401
+
+__all__ = ["ScratchtapeError", "lib", "MatRef", "Epilogue", "matmul", "matmul_f32", "matmul_with",
+           "f16_enabled", "f16_route"]

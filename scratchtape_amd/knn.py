@@ -1,0 +1,111 @@
+"""2-bit kNN memory on MI355X: the store, its device quantiser and the scored IVF search.
+
+Mirrors the quantised `KnnStore` (gpu_step/knn.rs:57-236) and the scored part of
+`KnnStore::search_ivf` (gpu_step/knn/ivf.rs:466-686) for 2-bit keys of width
+256: keys live cell-contiguous on the device (as `build_ivf` reorders them,
+ivf.rs:386-432), one f32 scale per key, codes packed 4 per byte.  The search
+takes each query's probed cells and returns, per query, the k nearest keys by
+the exact 2-bit score, ascending by (distance, key index), as global row
+indices with distances max(|q^|^2 + dist, 0) (ivf.rs:673-684).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .matmul import _stream
+
+KMAX = 128      # knn.rs:21
+PROBE_MAX = 16  # ivf.rs:126
+
+
+def _dptr(t: torch.Tensor, dtype: torch.dtype, what: str) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor")
+    if t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous {dtype} tensor")
+    return t.data_ptr()
+
+
+def quantize_2bit(keys: torch.Tensor, stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """tile_of for 2-bit keys (knn.rs:190-225) on the device: keys [n, d] -> (codes [n, d/4] u8, scales [n])."""
+    n, d = keys.shape
+    codes = torch.empty((n, d // 4), dtype=torch.uint8, device=keys.device)
+    scales = torch.empty(n, dtype=torch.float32, device=keys.device)
+    _lib.call("st_knn_quantize_2bit", _dptr(keys, torch.float32, "keys"), n, d, codes.data_ptr(),
+              scales.data_ptr(), _stream(stream))
+    return codes, scales
+
+
+def synth_store_2bit(seed: int, row0: int, codes: torch.Tensor, scales: torch.Tensor, stream=None) -> None:
+    """Fills codes/scales (rows row0.. of a synthetic store) with quantised N(0,1) keys (benchmark support)."""
+    n, kb = codes.shape
+    _lib.call("st_knn_synth_store_2bit", seed, row0, n, kb * 4, _dptr(codes, torch.uint8, "codes"),
+              _dptr(scales, torch.float32, "scales"), _stream(stream))
+
+
+def synth_keys_f32(seed: int, row0: int, n: int, d: int = 256, device="cuda", stream=None) -> torch.Tensor:
+    """The f32 keys synth_store_2bit quantises for rows row0..row0+n."""
+    keys = torch.empty((n, d), dtype=torch.float32, device=device)
+    _lib.call("st_knn_synth_keys_f32", seed, row0, n, d, keys.data_ptr(), _stream(stream))
+    return keys
+
+
+class KnnStore2bit:
+    """A cell-contiguous 2-bit key store on the device.
+
+    codes [N, d/4] uint8, scales [N] float32 (device tensors); cell_start [ncells+1]
+    int64 row offsets (host array; a device copy is kept for the scan).
+    """
+
+    def __init__(self, codes: torch.Tensor, scales: torch.Tensor, cell_start, d: int = 256):
+        if codes.dim() != 2 or codes.shape[1] * 4 != d:
+            raise ValueError("codes must be [N, d/4]")
+        if scales.shape != (codes.shape[0],):
+            raise ValueError("one scale per key")
+        cs = np.ascontiguousarray(np.asarray(cell_start, dtype=np.int64))
+        if cs.ndim != 1 or cs.size < 2 or cs[0] != 0 or cs[-1] != codes.shape[0] or np.any(np.diff(cs) < 0):
+            raise ValueError("cell_start must rise from 0 to the key count")
+        self.d = d
+        self.codes = codes
+        self.scales = scales
+        self.cell_start = cs
+        self.ncells = cs.size - 1
+        self.max_cell = int(np.diff(cs).max())
+        self.cell_start_dev = torch.from_numpy(cs).to(codes.device)
+
+    @classmethod
+    def from_keys(cls, keys: torch.Tensor, cell_start, stream=None) -> "KnnStore2bit":
+        """Quantises device keys [N, d] (already in cell order) into a store."""
+        codes, scales = quantize_2bit(keys, stream=stream)
+        return cls(codes, scales, cell_start, keys.shape[1])
+
+    def __len__(self) -> int:
+        return self.codes.shape[0]
+
+    def search_ivf(self, queries: torch.Tensor, probes: torch.Tensor, k: int = KMAX,
+                   out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, stream=None):
+        """Per query, the k nearest keys of its probed cells: (idx [nq, k] int64, dist [nq, k] float32).
+
+        queries [nq, d] float32, probes [nq, nprobe] int32 cell ids (device tensors).
+        """
+        nq, d = queries.shape
+        if d != self.d:
+            raise ValueError(f"queries have width {d}, the store {self.d}")
+        nprobe = probes.shape[1]
+        if probes.shape[0] != nq:
+            raise ValueError("one probe row per query")
+        if out is None:
+            idx = torch.empty((nq, k), dtype=torch.int64, device=queries.device)
+            dist = torch.empty((nq, k), dtype=torch.float32, device=queries.device)
+        else:
+            idx, dist = out
+        _lib.call("st_knn_search_ivf_2bit", _dptr(self.codes, torch.uint8, "codes"),
+                  _dptr(self.scales, torch.float32, "scales"), self.cell_start_dev.data_ptr(), self.ncells,
+                  self.max_cell, _dptr(queries, torch.float32, "queries"), _dptr(probes, torch.int32, "probes"),
+                  nq, nprobe, d, k, _dptr(idx, torch.int64, "idx"), _dptr(dist, torch.float32, "dist"),
+                  _stream(stream))
+        return idx, dist

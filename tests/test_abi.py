@@ -1,0 +1,72 @@
+"""CPU checks of the boundary: the library loads, exports every symbol the header
+declares, and the host-side mirrors validate arguments as the reference asserts."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import scratchtape_amd
+from scratchtape_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "scratchtape_hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(st_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    syms = header_symbols()
+    for name in ["st_matmul", "st_matmul_f32", "st_matmul_with", "st_ndarray_matmul", "st_softmax",
+                 "st_softmax_backward", "st_knn_quantize_2bit", "st_knn_search_ivf_2bit", "st_last_error"]:
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = scratchtape_amd.lib()
+    for name in header_symbols():
+        assert hasattr(L, name), name
+    # and the Python binding covers them all with argtypes
+    assert set(header_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_version_and_f16_switch():
+    L = scratchtape_amd.lib()
+    assert L.st_version().startswith(b"scratchtape_hip")
+    assert L.st_f16_enabled() in (0, 1)
+
+
+def test_struct_layouts_match_the_header():
+    # st_matref: p, off, stride, trans, reserved, ld, group, inner
+    assert _lib.StMatRef.inner.offset == 48 and _lib.ctypes.sizeof(_lib.StMatRef) == 56
+    assert _lib.StEpilogue.col_sum_stride.offset == 80 and _lib.ctypes.sizeof(_lib.StEpilogue) == 88
+
+
+def test_null_arguments_are_rejected_without_a_device():
+    L = scratchtape_amd.lib()
+    rc = L.st_matmul(None, None, None, 1, 1, 1, 1, None, None)
+    assert rc == _lib.ST_ERR_INVALID
+    assert b"NULL" in L.st_last_error()
+    rc = L.st_softmax(None, None, 4, 4, 4, 1.0, 1, 0, None)
+    assert rc == _lib.ST_ERR_INVALID
+
+
+def test_ndarray_matmul_shape_asserts_like_the_reference():
+    from scratchtape_amd.tensor import ndarray_matmul
+    with pytest.raises(ValueError, match="inner dims must match"):
+        ndarray_matmul(np.zeros((2, 3), np.float32), np.zeros((4, 2), np.float32))
+    with pytest.raises(ValueError, match="lhs must be 2D"):
+        ndarray_matmul(np.zeros(3, np.float32), np.zeros((3, 2), np.float32))
+
+
+def test_f16_route_mirrors_the_reference_pick():
+    from scratchtape_amd import f16_route
+    assert f16_route(128, 64, 64) and f16_route(128, 64, 96)
+    assert not f16_route(70, 64, 64)          # m ragged
+    assert not f16_route(64, 48, 64)          # k not a multiple of 32
+    assert not f16_route(64, 64, 64, col_sum=True, b_trans=True)
+    assert f16_route(4096, 256, 768)

@@ -1,0 +1,132 @@
+"""2-bit kNN memory on the GPU against the CPU oracle: quantiser bit-exact, and the
+IVF scan's per-query top-k index sets (and distances) bit-exact, ties broken by
+key index, from small edge cases up to the full 125M-key store."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from scratchtape_amd import knn
+
+pytestmark = pytest.mark.gpu
+D = 256
+
+
+def test_quantizer_is_bit_exact(dev):
+    rng = np.random.default_rng(1)
+    keys = rng.standard_normal((5000, D)).astype(np.float32)
+    keys[0] = 0.0                      # scale floor 1e-30
+    keys[1] *= 1e-20                   # tiny
+    keys[2] *= 1e10                    # huge
+    keys[3, :] = 0.75 * np.tile([1, -1], D // 2)  # codes 3/0 exactly
+    keys[4] = np.where(np.arange(D) < 3, 100.0, 0.001)  # clamping
+    codes, scales = knn.quantize_2bit(torch.from_numpy(keys).to(dev))
+    wc, ws = oracle.quantize_2bit(keys, D)
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    np.testing.assert_array_equal(scales.cpu().numpy(), ws)
+
+
+def test_synthetic_store_is_the_quantised_synthetic_keys(dev):
+    n, row0, seed = 3000, 123_456_789, 7
+    keys = knn.synth_keys_f32(seed, row0, n, D, device=dev)
+    codes = torch.empty((n, D // 4), dtype=torch.uint8, device=dev)
+    scales = torch.empty(n, dtype=torch.float32, device=dev)
+    knn.synth_store_2bit(seed, row0, codes, scales)
+    k = keys.cpu().numpy()
+    assert abs(k.mean()) < 0.01 and abs(k.var() - 1) < 0.01
+    wc, ws = oracle.quantize_2bit(k, D)
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    np.testing.assert_array_equal(scales.cpu().numpy(), ws)
+
+
+def make_store(dev, sizes, seed):
+    cell_start = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    keys = np.random.default_rng(seed).standard_normal((int(cell_start[-1]), D)).astype(np.float32)
+    store = knn.KnnStore2bit.from_keys(torch.from_numpy(keys).to(dev), cell_start)
+    return store, store.codes.cpu().numpy(), store.scales.cpu().numpy(), cell_start
+
+
+def check_search(dev, store, codes, scales, cell_start, queries, probes, k):
+    idx, dist = store.search_ivf(torch.from_numpy(queries).to(dev), torch.from_numpy(probes).to(dev), k)
+    widx, wdist = oracle.knn_search(codes, scales, cell_start, queries, probes, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), widx)
+    np.testing.assert_array_equal(dist.cpu().numpy(), wdist)
+    return widx
+
+
+def test_search_small_with_edge_cases(dev):
+    rng = np.random.default_rng(2)
+    ncells = 40
+    sizes = rng.integers(0, 3000, ncells)
+    sizes[0], sizes[1], sizes[2] = 0, 3, 1000  # empty cell, tiny cell
+    store, codes, scales, cs = make_store(dev, sizes, 3)
+    nq = 64
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    queries[0] = 0.0  # zero query: qs = 1, every Q is 0
+    queries[1] *= 1e6
+    probes = np.stack([rng.choice(ncells, 8, replace=False) for _ in range(nq)]).astype(np.int32)
+    probes[2] = [0, 1, 0, 1, 0, 1, 0, 1]  # three keys in total: padding
+    probes[3, 5] = probes[3, 1]          # a repeated cell is scanned once
+    for k in (128, 10, 1):
+        widx = check_search(dev, store, codes, scales, cs, queries, probes, k)
+    idx, dist = store.search_ivf(torch.from_numpy(queries).to(dev), torch.from_numpy(probes).to(dev), 128)
+    idx = idx.cpu().numpy()
+    assert sorted(idx[2][:3]) == [0 + sizes[0], 1 + sizes[0], 2 + sizes[0]] and np.all(idx[2][3:] == -1)
+
+
+def test_search_ties_break_by_key_index(dev):
+    # Identical keys give identical scores: the kept ones must be the lowest indices.
+    base = np.random.default_rng(4).standard_normal(D).astype(np.float32)
+    keys = np.tile(base, (700, 1))
+    cs = np.array([0, 300, 700], np.int64)
+    store = knn.KnnStore2bit.from_keys(torch.from_numpy(keys).to(dev), cs)
+    q = np.random.default_rng(5).standard_normal((2, D)).astype(np.float32)
+    probes = np.array([[1, 0], [0, 1]], np.int32)
+    idx, _ = store.search_ivf(torch.from_numpy(q).to(dev), torch.from_numpy(probes).to(dev), 128)
+    np.testing.assert_array_equal(idx.cpu().numpy(), np.tile(np.arange(128), (2, 1)))
+
+
+def test_search_cells_of_the_benchmark_size(dev):
+    # Cells of ~10.2k keys (125M / 12288), 8 probes per query.
+    rng = np.random.default_rng(6)
+    ncells = 48
+    sizes = rng.poisson(10172, ncells)
+    store, codes, scales, cs = make_store(dev, sizes, 7)
+    nq = 48
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, 8, replace=False) for _ in range(nq)]).astype(np.int32)
+    check_search(dev, store, codes, scales, cs, queries, probes, 128)
+
+
+def test_full_store_125m_keys(dev):
+    """The benchmark's store: 125M keys in 12288 cells, 256 queries x 8 probes; 6 queries checked exactly."""
+    n, ncells, nq, nprobe, seed = 125_000_000, 12288, 256, 8, 11
+    rng = np.random.default_rng(seed)
+    sizes = rng.multinomial(n, np.full(ncells, 1.0 / ncells))
+    cs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    codes = torch.empty((n, D // 4), dtype=torch.uint8, device=dev)
+    scales = torch.empty(n, dtype=torch.float32, device=dev)
+    knn.synth_store_2bit(seed, 0, codes, scales)
+    store = knn.KnnStore2bit(codes, scales, cs)
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, nprobe, replace=False) for _ in range(nq)]).astype(np.int32)
+    idx, dist = store.search_ivf(torch.from_numpy(queries).to(dev), torch.from_numpy(probes).to(dev), 128)
+    idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+    for qi in [0, 1, 77, 128, 200, 255]:
+        cells = probes[qi]
+        rows = [np.arange(cs[c], cs[c + 1]) for c in cells]
+        sub_cs = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+        allrows = np.concatenate(rows)
+        sel = torch.from_numpy(allrows).to(dev)
+        sc = codes[sel].cpu().numpy()
+        ss = scales[sel].cpu().numpy()
+        widx, wdist = oracle.knn_search(sc, ss, sub_cs, queries[qi:qi + 1],
+                                        np.arange(nprobe, dtype=np.int32)[None, :], 128)
+        np.testing.assert_array_equal(idx[qi], allrows[widx[0]])
+        np.testing.assert_array_equal(dist[qi], wdist[0])
+    # every result lies in its query's probed cells and is sorted
+    assert np.all(np.diff(dist, axis=1) >= 0)
+    cell_of = np.searchsorted(cs, idx, side="right") - 1
+    assert np.all(np.any(cell_of[:, :, None] == probes[:, None, :], axis=2))
+    del codes, scales, store
+    torch.cuda.empty_cache()
