@@ -338,7 +338,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["all", "gemm", "knn"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy 10 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.calib_copy:
+        import torch
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes_each_way": src.numel() * 4, "dispatches": 10}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X (asked for --gpus {args.gpus}); "
               "see the sharding design for more than one", file=sys.stderr)
@@ -416,7 +427,7 @@ def main():
         knn = dict(ms_per_batch=round(ms, 5), keys_per_s=round(pairs / ms * 1e3, 1),
                    g_keys_per_s=round(pairs / ms / 1e6, 3), pairs_per_batch=int(pairs),
                    distinct_cell_bytes=int(byts), hbm_gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK["hbm_gbs"], 4),
-                   roofline=dict(kernel="st_knn_search_ivf_2bit (k_prep + k_scan + k_merge)", bound="hbm",
+                   roofline=dict(kernel="k_search (st_knn_search_ivf_2bit: one fused launch)", bound="hbm",
                                  achieved=round(gbs, 1), peak=PEAK["hbm_gbs"], unit="GB/s",
                                  frac=round(gbs / PEAK["hbm_gbs"], 4), traffic=None),
                    store_gen_s=round(kb.gen_s, 3))

@@ -346,9 +346,9 @@ void orc_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t *codes, 
 /* Exact 2-bit scoring contract (the build's replacement for the reference's */
 /* f16 cmma dots, ivf.rs:249-321, and distance, ivf.rs:235).                 */
 /*                                                                            */
-/* Query q (f32, d) -> power-of-two scale qs = 2^(E-15) where M = max|q_i| = */
+/* Query q (f32, d) -> power-of-two scale qs = 2^(E-14) where M = max|q_i| = */
 /* m * 2^E, m in [0.5, 1) (qs = 1 when M == 0); Q_i = clamp(rint(q_i / qs),  */
-/* -32767, 32767) (exact: qs is a power of two).  Key code u_i in 0..3 and   */
+/* -16384, 16384) (exact: qs is a power of two).  Key code u_i in 0..3 and   */
 /* scale s decode to k_i = (u_i - 1.5) s = c_i s / 2 with c_i = 2u_i - 3.     */
 /*   dot  = sum c_i Q_i                (exact int32)                          */
 /*   c2   = sum c_i^2 = 256-ish..      (exact int32)                          */
@@ -376,14 +376,14 @@ void orc_knn_prep_query(const float *q, int64_t d, int16_t *Q, orc_qprep *prep) 
     if (mx > 0.0f) {
         int e;
         frexpf(mx, &e);
-        qs = ldexpf(1.0f, e - 15);
+        qs = ldexpf(1.0f, e - 14);
     }
     int64_t sq2 = 0;
     int32_t sq = 0;
     for (int64_t i = 0; i < d; i++) {
         float v = rintf(q[i] / qs);
-        if (v > 32767.0f) v = 32767.0f;
-        if (v < -32767.0f) v = -32767.0f;
+        if (v > 16384.0f) v = 16384.0f;
+        if (v < -16384.0f) v = -16384.0f;
         int32_t x = (int32_t)v;
         Q[i] = (int16_t)x;
         sq += x;

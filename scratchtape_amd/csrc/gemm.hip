@@ -16,8 +16,11 @@
 //    so the 128-bit fragment reads of 8 lanes hit distinct banks).  An operand
 //    whose k is contiguous in memory (A not transposed, B transposed) is copied
 //    as vectors; the others are loaded as 4x4 blocks and transposed in
-//    registers.  Two LDS stages: the next k-stage is fetched into registers
-//    while the current one feeds the MFMAs, one barrier per stage.
+//    registers.  k-stages of 64 (f16) / 32 (f32); two LDS buffers and two
+//    register sets, so stage s+2 is in flight from global memory while stage s
+//    feeds the MFMAs and stage s+1 is written to LDS; one barrier per stage.
+//  - Workgroups are remapped so that each of the 8 XCDs works on a contiguous
+//    run of tiles, which share operand panels in that XCD's L2.
 //  - Fragment k-order: each lane reads its k-run as one 128-bit LDS read and
 //    feeds it to the MFMA; A and B use the same k mapping, so the dot product
 //    is over the right pairs whatever order the hardware sums them in.
@@ -160,6 +163,13 @@ struct Stager {
         }
     }
 
+    __device__ __forceinline__ void merge_cs(const Stager &o) {
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+#pragma unroll
+            for (int x = 0; x < (KCONTIG ? 1 : 4); x++) cs[i][x] += o.cs[i][x];
+    }
+
     // Writes this thread's column-sum partials to red[col * SLOTS + slot].
     __device__ __forceinline__ void put_cs(float *red, int tid) const {
 #pragma unroll
@@ -192,21 +202,33 @@ __global__ __launch_bounds__(THREADS) void k_gemm(GemmArgs g) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int64_t z = blockIdx.z;
+    // Workgroups are dealt to the 8 XCDs round-robin by linear id; remap so
+    // each XCD gets a contiguous run of tiles (x fastest), which share A rows
+    // (and k-slices) in that XCD's L2.
+    int64_t lin = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+    const int64_t total = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+    const int bx = (int)(lin % gridDim.x);
+    const int by = (int)((lin / gridDim.x) % gridDim.y);
+    const int64_t z = lin / ((int64_t)gridDim.x * gridDim.y);
     const int64_t zb = z / g.splits;
     const int slice = (int)(z % g.splits);
-    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    const int row0 = by * BM, col0 = bx * BN;
     const int kbeg = slice * g.slice_k;
     const int kend = min(g.k, kbeg + g.slice_k);
     const int nst = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
     const float *abase = g.a.p + mat_base(g.a, zb);
     const float *bbase = g.b.p + mat_base(g.b, zb);
-    const bool do_cs = g.has_cs && blockIdx.y == 0;
+    const bool do_cs = g.has_cs && by == 0;
 
-    SA sa;
-    SB sb;
-    sb.zero_cs();
+    // Two register sets: stage st+2 is fetched into the set stage st came
+    // from while stage st is multiplied out of LDS, so two stages of global
+    // loads are in flight behind every barrier.
+    SA sa[2];
+    SB sb[2];
+    sb[0].zero_cs();
+    sb[1].zero_cs();
     f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
@@ -214,24 +236,29 @@ __global__ __launch_bounds__(THREADS) void k_gemm(GemmArgs g) {
         for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (nst > 0) {
-        sa.load(abase, g.a.ld, row0, g.m, kbeg, kend, tid);
-        sb.load(bbase, g.b.ld, col0, g.n, kbeg, kend, tid);
-        if (do_cs) sb.add_cs();
-        sa.store(As[0], tid);
-        sb.store(Bs[0], tid);
+        sa[0].load(abase, g.a.ld, row0, g.m, kbeg, kend, tid);
+        sb[0].load(bbase, g.b.ld, col0, g.n, kbeg, kend, tid);
+    }
+    if (nst > 1) {
+        sa[1].load(abase, g.a.ld, row0, g.m, kbeg + BK, kend, tid);
+        sb[1].load(bbase, g.b.ld, col0, g.n, kbeg + BK, kend, tid);
+    }
+    if (nst > 0) {
+        if (do_cs) sb[0].add_cs();
+        sa[0].store(As[0], tid);
+        sb[0].store(Bs[0], tid);
     }
     __syncthreads();
 
-    for (int st = 0; st < nst; st++) {
-        const int buf = st & 1;
-        const bool more = st + 1 < nst;
-        if (more) {
-            const int k0 = kbeg + (st + 1) * BK;
-            sa.load(abase, g.a.ld, row0, g.m, k0, kend, tid);
-            sb.load(bbase, g.b.ld, col0, g.n, k0, kend, tid);
+    auto body = [&](auto pc, int st) {
+        constexpr int P = decltype(pc)::value;
+        if (st + 2 < nst) {
+            const int k0 = kbeg + (st + 2) * BK;
+            sa[P].load(abase, g.a.ld, row0, g.m, k0, kend, tid);
+            sb[P].load(bbase, g.b.ld, col0, g.n, k0, kend, tid);
         }
-        const T *as = As[buf] + (wm * WM + (lane & 15)) * LDS_K;
-        const T *bs = Bs[buf] + (wn * WN + (lane & 15)) * LDS_K;
+        const T *as = As[P] + (wm * WM + (lane & 15)) * LDS_K;
+        const T *bs = Bs[P] + (wn * WN + (lane & 15)) * LDS_K;
         if constexpr (F16) {
 #pragma unroll
             for (int ks = 0; ks < BK / 32; ks++) {
@@ -265,19 +292,24 @@ __global__ __launch_bounds__(THREADS) void k_gemm(GemmArgs g) {
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
             }
         }
-        if (more) {
-            if (do_cs) sb.add_cs();
-            sa.store(As[buf ^ 1], tid);
-            sb.store(Bs[buf ^ 1], tid);
+        if (st + 1 < nst) {
+            if (do_cs) sb[P ^ 1].add_cs();
+            sa[P ^ 1].store(As[P ^ 1], tid);
+            sb[P ^ 1].store(Bs[P ^ 1], tid);
         }
         __syncthreads();
+    };
+    for (int st = 0; st < nst; st += 2) {
+        body(std::integral_constant<int, 0>(), st);
+        if (st + 1 < nst) body(std::integral_constant<int, 1>(), st + 1);
     }
 
     // Column sums of this slice of B (tile row 0 only), reduced in slot order.
     if (do_cs) {
         float *red = reinterpret_cast<float *>(As[0]);  // BN * SLOTS floats fit in As
         static_assert(BN * SB::SLOTS * 4 <= BM * LDS_K * (int)sizeof(T), "column-sum buffer");
-        sb.put_cs(red, tid);
+        sb[0].merge_cs(sb[1]);
+        sb[0].put_cs(red, tid);
         __syncthreads();
         if (tid < BN && col0 + tid < g.n) {
             float tot = 0.f;
@@ -415,7 +447,7 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
     const int64_t ldo = out->ld ? out->ld : n;
 
     TileCfg tc = choose_tile(batch, m, n);
-    const int BK = f16 ? 32 : 16;
+    const int BK = f16 ? 64 : 32;
     const int64_t tiles = batch * cdiv(m, tc.bm) * cdiv(n, tc.bn);
 
     // Split-k as the reference allows it (matmul.rs:117-123): no epilogue but
@@ -481,13 +513,13 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
                       aligned4(a->p, a->off, a->stride, a->inner, lda) && aligned4(b->p, b->off, b->stride, b->inner, ldb);
     KernelFn fn;
     if (f16) {
-        if (tc.bm == 128 && tc.bn == 128) fn = pick_kernel<128, 128, 32, true>(a->trans, b->trans, fast);
-        else if (tc.bm == 128) fn = pick_kernel<128, 64, 32, true>(a->trans, b->trans, fast);
-        else fn = pick_kernel<64, 64, 32, true>(a->trans, b->trans, fast);
+        if (tc.bm == 128 && tc.bn == 128) fn = pick_kernel<128, 128, 64, true>(a->trans, b->trans, fast);
+        else if (tc.bm == 128) fn = pick_kernel<128, 64, 64, true>(a->trans, b->trans, fast);
+        else fn = pick_kernel<64, 64, 64, true>(a->trans, b->trans, fast);
     } else {
-        if (tc.bm == 128 && tc.bn == 128) fn = pick_kernel<128, 128, 16, false>(a->trans, b->trans, fast);
-        else if (tc.bm == 128) fn = pick_kernel<128, 64, 16, false>(a->trans, b->trans, fast);
-        else fn = pick_kernel<64, 64, 16, false>(a->trans, b->trans, fast);
+        if (tc.bm == 128 && tc.bn == 128) fn = pick_kernel<128, 128, 32, false>(a->trans, b->trans, fast);
+        else if (tc.bm == 128) fn = pick_kernel<128, 64, 32, false>(a->trans, b->trans, fast);
+        else fn = pick_kernel<64, 64, 32, false>(a->trans, b->trans, fast);
     }
     dim3 grid((unsigned)cdiv(n, tc.bn), (unsigned)cdiv(m, tc.bm), (unsigned)(batch * splits));
     hipLaunchKernelGGL(fn, grid, dim3(THREADS), 0, stream, g);

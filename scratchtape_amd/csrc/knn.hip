@@ -1,5 +1,5 @@
-// 2-bit kNN memory on gfx950: device quantiser, fused dequant-dot scan with
-// exact integer scoring, streaming per-(query, cell) top-128, per-query merge.
+// 2-bit kNN memory on gfx950: device quantiser and the fused IVF search
+// (exact integer 2-bit scoring + exact per-query top-k in one kernel).
 //
 // Reference: gpu_step/knn.rs:190-225 (tile_of: the 2-bit quantiser),
 // knn.rs:628-643 (k_dequant: code u decodes to (u - 1.5) * scale),
@@ -8,32 +8,37 @@
 // finalisation (dd + |q|^2).max(0) (ivf.rs:673-684).
 //
 // Scoring contract (replaces the reference's f16 x f16 -> f32 cmma dots, whose
-// accumulation order no CPU can reproduce): the query is quantised to int16
-// with a power-of-two scale qs, Q_i = clamp(rint(q_i / qs), +-32767), and with
-// c_i = 2u_i - 3 the key decodes to c_i * s / 2.  Then
+// accumulation order no CPU can reproduce): the query is quantised with a
+// power-of-two scale qs = 2^(E-14) (max|q| = m 2^E, m in [0.5, 1)),
+// Q_i = clamp(rint(q_i / qs), +-16384), and with c_i = 2u_i - 3 the key
+// decodes to c_i * s / 2.  Then
 //     dot  = sum c_i Q_i        (exact, int32)
 //     c2   = sum c_i^2          (exact, int32)
 //     dist = ((s*s)*0.25f)*(float)c2 - (s*qs)*(float)dot
 // with every f32 operation separately rounded (contraction off), which the CPU
 // oracle reproduces bit for bit.  Ranking is by (dist, key index) ascending.
 //
-// Scan design: one 256-thread workgroup per (query, probed cell).  A wave
-// reads 64 keys (4 KB of codes) per iteration as four fully coalesced 1 KB
-// loads: lane l holds bytes 16*(l%4).. of key 16*s + l/4, i.e. 4 of the key's
-// 16 code dwords, so each lane keeps only its quarter of the packed query (32
-// VGPRs) and no LDS reads sit in the inner loop.  Per code dword:
-// 4 masked shifts give bytes u in 0..3, one v_dot4_i32_i8 against the query's
-// high bytes and one v_dot4_u32_u8 against its low bytes per shift, and one
-// popcount for c2.  The four quarter-sums are combined with two butterfly
-// shuffles (integer, so exact in any order).
+// Search design: one 1024-thread workgroup (16 wave64s) per query streams the
+// concatenation of its probed cells, 1024 keys (64 KB of codes) per iteration
+// with the next iteration's loads in flight.  Lane l handles bytes 16*(l%4)..
+// of a key (4 of its 16 code dwords), so a wave's loads are fully coalesced
+// 1 KB rows and each lane keeps only its quarter of the query in registers.
+// The query is held as balanced base-16 digits (Q = d0 + 16 d1 + 256 d2 +
+// 4096 d3, d in [-8, 7]); per code dword two masks give the codes as 4-bit
+// nibbles and eight v_dot8_i32_i4 (one per digit and nibble set) accumulate
+// the exact dot, one popcount gives c2.  The four quarter sums are combined
+// with two butterfly shuffles (integers: exact in any order).
 //
-// Top-k: candidates with key64 = (ordered dist bits << 32 | index) below the
-// workgroup's threshold tau are appended to an LDS buffer of 1024; when it
-// nears full, a bitonic sort keeps the 128 smallest and tau becomes the 128th.
-// Only keys with at least 128 smaller keys already seen are ever dropped, so
-// the cell's exact top-128 survives whatever the append order; the final sort
-// makes the list deterministic.  A merge kernel sorts each query's nprobe lists
-// and keeps the k best.
+// Top-k: each wave appends candidates with key64 = (ordered dist bits << 32 |
+// index) below its threshold to its own LDS list (ballot + mbcnt, no atomics,
+// no workgroup barrier in the scan); when the list fills (or after the first
+// 256 candidates) a wave-level bitonic sort keeps its 128 smallest and its
+// threshold becomes the 128th, published to the workgroup through an LDS
+// atomicMin.  Only keys with at least 128 smaller keys already seen are
+// dropped, so the exact top-128 survives whatever the order, and the final
+// sort makes the result deterministic.  Cells that other queries of the
+// batch also probe are scanned first, so their bytes are read while the other
+// workgroups still find them in the MALL.
 #include <cstring>
 
 #include "common.h"
@@ -45,15 +50,10 @@ namespace {
 constexpr int D = 256;          // key width handled by the scan
 constexpr int DW = D / 16;      // code dwords per key
 constexpr int KMAX = 128;       // neighbours kept per query (knn.rs:21)
-constexpr int CAP = 1024;       // LDS candidate buffer (entries)
+constexpr int CAPW = 512;       // LDS candidate list per wave (entries)
+constexpr int FIN = 4096;       // LDS starting set + final gather (entries)
 constexpr int PROBE_MAX = 16;   // most cells one query probes (ivf.rs:126)
-constexpr int QPACK = 136;      // dwords per prepared query: 128 packed bytes + 4 scalars + pad
 constexpr uint64_t NONE = ~0ull;
-
-struct QScalars {
-    float qs, qn;
-    int32_t sq, pad;
-};
 
 __device__ __forceinline__ uint32_t fkey(float f) {
     uint32_t x = __float_as_uint(f);
@@ -133,67 +133,24 @@ __global__ __launch_bounds__(256) void k_synth_keys(uint64_t seed, int64_t row0,
     keys[e] = synth_gauss(seed, row0 + e / d, (int)(e % d));
 }
 
-// ---------------------------------------------------------------- query prep
+// ---------------------------------------------------------------- fused search
 
-// One wave per query: the int16 quantisation, then the bytes packed for the
-// scan: dword (v, t, h) of code dword v holds, in byte j, the high (h = 0,
-// signed) or low (h = 1, unsigned) byte of Q[16v + 4j + t], matching the
-// bytes (w >> 2t) & 0x03030303 extracts from code dword v.
-__global__ __launch_bounds__(64) void k_prep(const float *__restrict__ queries, uint32_t *__restrict__ qpack) {
-    __shared__ uint8_t bytes[DW * 4 * 2 * 4];
-    const int q = blockIdx.x, lane = threadIdx.x;
-    const float4 v = reinterpret_cast<const float4 *>(queries + (int64_t)q * D)[lane];
-    const float x[4] = {v.x, v.y, v.z, v.w};
-    float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+constexpr int SW = 16;          // waves per search workgroup
+constexpr int STH = SW * 64;    // threads per search workgroup (one workgroup per query)
+constexpr int KPI = STH;        // keys scanned per iteration: 4 lanes per key, 4 sub-steps
+
+__device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float qs = 1.f, inv = 1.f;
-    if (mx > 0.f) {
-        int e;
-        frexpf(mx, &e);
-        qs = ldexpf(1.f, e - 15);
-        inv = ldexpf(1.f, 15 - e);
-    }
-    int32_t sq = 0;
-    double sq2 = 0.0;
-    const int dwv = lane >> 2, j = lane & 3;  // dims 4*lane + t = 16*dwv + 4*j + t
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        float r = rintf(x[t] * inv);
-        r = fminf(fmaxf(r, -32767.f), 32767.f);
-        const int32_t Q = (int32_t)r;
-        sq += Q;
-        sq2 += (double)Q * (double)Q;
-        bytes[((dwv * 4 + t) * 2 + 0) * 4 + j] = (uint8_t)((Q >> 8) & 0xff);
-        bytes[((dwv * 4 + t) * 2 + 1) * 4 + j] = (uint8_t)(Q & 0xff);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        sq += __shfl_xor(sq, o, 64);
-        sq2 += __shfl_xor(sq2, o, 64);
-    }
-    __syncthreads();
-    uint32_t *dst = qpack + (int64_t)q * QPACK;
-    dst[lane] = reinterpret_cast<const uint32_t *>(bytes)[lane];
-    dst[lane + 64] = reinterpret_cast<const uint32_t *>(bytes)[lane + 64];
-    if (lane == 0) {
-        QScalars s;
-        s.qs = qs;
-        s.qn = (float)sq2 * (qs * qs);
-        s.sq = sq;
-        s.pad = 0;
-        *reinterpret_cast<QScalars *>(dst + 128) = s;
-    }
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
 }
 
-// ---------------------------------------------------------------- bitonic sort in LDS
-
-// Sorts buf[0..n) ascending (n a power of two, <= 2048) with all 256 threads.
+// Sorts buf[0..n) ascending (n a power of two) with all threads of the block.
 __device__ void bitonic_sort(uint64_t *buf, int n) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
     for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < n; i += 256) {
+            for (int i = tid; i < n; i += nt) {
                 const int ixj = i ^ j;
                 if (ixj > i) {
                     const uint64_t a = buf[i], b = buf[ixj];
@@ -209,144 +166,338 @@ __device__ void bitonic_sort(uint64_t *buf, int n) {
     }
 }
 
+// Sorts buf[0..n) ascending (n a power of two) within one wave: LDS operations
+// of a wave complete in order, so the stages need no barrier, only a fence that
+// keeps the compiler from reordering them.
+__device__ void wave_sort(uint64_t *buf, int n, int lane) {
+    for (int k = 2; k <= n; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = lane; i < n; i += 64) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t a = buf[i], b = buf[ixj];
+                    const bool up = (i & k) == 0;
+                    if ((a > b) == up) {
+                        buf[i] = b;
+                        buf[ixj] = a;
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 __device__ __forceinline__ int pow2_at_least(int x) {
     int n = KMAX;
     while (n < x) n <<= 1;
     return n;
 }
 
-// ---------------------------------------------------------------- scan
-
-__device__ __forceinline__ void quarter_dot(const uint4 &c, const uint32_t (&qh)[4][4], const uint32_t (&ql)[4][4],
-                                            int32_t &hi, uint32_t &lo, uint32_t &n12) {
+// One lane's quarter of a key (code dwords 4*quarter .. +3) against the
+// query's balanced base-16 digits: acc[p] gathers sum u*digit_p over the
+// quarter, n12 the codes with u in {1, 2}.
+__device__ __forceinline__ void quarter_dot(const uint4 &c, const uint32_t (&qd)[4][2][4], int32_t (&acc)[4],
+                                            uint32_t &n12) {
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
     for (int v = 0; v < 4; v++) {
+        const uint32_t ea = w[v] & 0x33333333u;         // nibble j: code 2j
+        const uint32_t eb = (w[v] >> 2) & 0x33333333u;  // nibble j: code 2j + 1
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const uint32_t e = (w[v] >> (2 * t)) & 0x03030303u;
-            hi = __builtin_amdgcn_sdot4((int)e, (int)qh[v][t], hi, false);
-            lo = __builtin_amdgcn_udot4(e, ql[v][t], lo, false);
+        for (int p = 0; p < 4; p++) {
+            acc[p] = __builtin_amdgcn_sdot8((int)ea, (int)qd[v][0][p], acc[p], false);
+            acc[p] = __builtin_amdgcn_sdot8((int)eb, (int)qd[v][1][p], acc[p], false);
         }
         n12 += __popc((w[v] ^ (w[v] >> 1)) & 0x55555555u);
     }
 }
 
-// grid: nq * nprobe workgroups of 256; workgroup (q, p) scans cell probes[q, p].
-__global__ __launch_bounds__(256) void k_scan(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
-                                              const int64_t *__restrict__ cell_start, int64_t ncells,
-                                              const int32_t *__restrict__ probes, int32_t nprobe,
-                                              const uint32_t *__restrict__ qpack, uint64_t *__restrict__ lists) {
-    __shared__ uint64_t cand[CAP];
-    __shared__ int count;
+// grid: one workgroup of 1024 threads per query.
+__global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const float *scales,
+                                                const int64_t *__restrict__ cell_start, int64_t ncells,
+                                                const float *__restrict__ queries, const int32_t *__restrict__ probes,
+                                                int32_t nq, int32_t nprobe, int32_t k, int64_t *__restrict__ out_idx,
+                                                float *__restrict__ out_dist) {
+    __shared__ uint64_t cand[SW * CAPW];  // per-wave candidate lists
+    __shared__ uint64_t fin[FIN];         // the starting set and the final gather
+    __shared__ uint64_t s_tau;            // min over the waves' thresholds
+    __shared__ int8_t dig[4][D];
+    __shared__ uint32_t qpk[DW * 2 * 4];
+    __shared__ float s_qs, s_qn;
+    __shared__ int32_t s_sq, s_np, count;
+    __shared__ int32_t s_cell[PROBE_MAX], s_share[PROBE_MAX];
+    __shared__ int64_t s_r0[PROBE_MAX];
+    __shared__ int32_t s_len[PROBE_MAX], s_cpre[PROBE_MAX + 1];
+
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t pair = blockIdx.x;
-    const int64_t q = pair / nprobe;
-    const int p = (int)(pair % nprobe);
-    uint64_t *out = lists + pair * KMAX;
+    const int64_t q = blockIdx.x;
 
-    const int32_t cell = probes[pair];
-    bool skip = cell < 0 || cell >= ncells;
-    for (int pp = 0; pp < p; pp++) skip |= probes[q * nprobe + pp] == cell;
-    if (skip) {
-        if (tid < KMAX) out[tid] = NONE;
-        return;
-    }
-    const int64_t r0 = cell_start[cell], r1 = cell_start[cell + 1];
-
-    // This lane's quarter of the packed query: code dwords 4*(lane%4) + v.
-    const uint32_t *qp = qpack + q * QPACK;
-    uint32_t qh[4][4], ql[4][4];
-    const int quarter = lane & 3;
-#pragma unroll
-    for (int v = 0; v < 4; v++)
+    if (wave == 0) {
+        // Query quantisation: qs = 2^(E-14) with max|q| = m 2^E, Q = clamp(rint(q / qs), +-16384),
+        // then balanced base-16 digits d0..d3 in [-8, 7] with Q = d0 + 16 d1 + 256 d2 + 4096 d3.
+        const float4 v = reinterpret_cast<const float4 *>(queries + q * D)[lane];
+        const float x[4] = {v.x, v.y, v.z, v.w};
+        const float mx = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+        float qs = 1.f, inv = 1.f;
+        if (mx > 0.f) {
+            int e;
+            frexpf(mx, &e);
+            qs = ldexpf(1.f, e - 14);
+            inv = ldexpf(1.f, 14 - e);
+        }
+        int32_t sq = 0;
+        double sq2 = 0.0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            qh[v][t] = qp[((4 * quarter + v) * 4 + t) * 2 + 0];
-            ql[v][t] = qp[((4 * quarter + v) * 4 + t) * 2 + 1];
-        }
-    const QScalars qsc = *reinterpret_cast<const QScalars *>(qp + 128);
-    const int32_t c2_base = 9 * D;
-
-    if (tid == 0) count = 0;
-    uint64_t tau = NONE;
-    __syncthreads();
-
-    const uint4 *cbase = reinterpret_cast<const uint4 *>(codes);
-    uint4 cur[4], nxt[4];
-    auto load = [&](uint4 (&dst)[4], int64_t base) {
+            const float r = fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16384.f);
+            int32_t Q = (int32_t)r;
+            sq += Q;
+            sq2 += (double)Q * (double)Q;
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int64_t key = base + wave * 64 + s * 16 + (lane >> 2);
-            dst[s] = key < r1 ? cbase[key * 4 + quarter] : make_uint4(0, 0, 0, 0);
-        }
-    };
-    load(cur, r0);
-    for (int64_t base = r0; base < r1; base += 256) {
-        if (base + 256 < r1) load(nxt, base + 256);
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int64_t key = base + wave * 64 + s * 16 + (lane >> 2);
-            int32_t hi = 0;
-            uint32_t lo = 0, n12 = 0;
-            quarter_dot(cur[s], qh, ql, hi, lo, n12);
-            int32_t duq = hi * 256 + (int32_t)lo;
-            duq += __shfl_xor(duq, 1, 64);
-            duq += __shfl_xor(duq, 2, 64);
-            n12 += __shfl_xor(n12, 1, 64);
-            n12 += __shfl_xor(n12, 2, 64);
-            if (quarter == 0 && key < r1) {
-                const float sc = scales[key];
-                const int32_t dot = 2 * duq - 3 * qsc.sq;
-                const int32_t c2 = c2_base - 8 * (int32_t)n12;
-                const float t1 = (sc * sc) * 0.25f * (float)c2;
-                const float t3 = (sc * qsc.qs) * (float)dot;
-                const float dist = t1 - t3 + 0.0f;
-                const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)key;
-                if (k64 < tau) cand[atomicAdd(&count, 1)] = k64;
+            for (int p = 0; p < 4; p++) {
+                const int32_t d = p < 3 ? ((Q + 8) & 15) - 8 : Q;
+                dig[p][4 * lane + t] = (int8_t)d;
+                Q = (Q - d) >> 4;
             }
         }
 #pragma unroll
-        for (int s = 0; s < 4; s++) cur[s] = nxt[s];
-        __syncthreads();  // this iteration's appends are done
-        const int cnt = count;
-        __syncthreads();  // everyone has read count before the next appends
-        if (cnt > CAP - 256) {
-            const int n = pow2_at_least(cnt);
-            for (int i = cnt + tid; i < n; i += 256) cand[i] = NONE;
-            __syncthreads();
-            bitonic_sort(cand, n);
-            tau = cand[KMAX - 1];
-            __syncthreads();
-            if (tid == 0) count = KMAX;
-            __syncthreads();
+        for (int o = 32; o > 0; o >>= 1) {
+            sq += __shfl_xor(sq, o, 64);
+            sq2 += __shfl_xor(sq2, o, 64);
+        }
+        if (lane == 0) {
+            s_qs = qs;
+            s_qn = (float)sq2 * (qs * qs);
+            s_sq = sq;
+        }
+    } else {
+        // How many (query, probe) pairs of the whole batch scan each probed cell.
+        for (int j = wave - 1; j < nprobe; j += SW - 1) {
+            const int32_t cell = probes[q * nprobe + j];
+            int cnt = 0;
+            for (int64_t i = lane; i < (int64_t)nq * nprobe; i += 64) cnt += probes[i] == cell;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+            if (lane == 0) {
+                s_cell[j] = cell;
+                s_share[j] = cnt;
+            }
         }
     }
+    __syncthreads();
+    if (tid == 0) {
+        // Cells scanned by several queries of the batch first (their bytes are
+        // then read while still in the MALL), a repeated cell once, invalid ids
+        // skipped; s_pre holds the running key count.
+        int order[PROBE_MAX];
+        for (int j = 0; j < nprobe; j++) {
+            int i = j;
+            while (i > 0 && (s_share[order[i - 1]] < s_share[j] ||
+                             (s_share[order[i - 1]] == s_share[j] && s_cell[order[i - 1]] > s_cell[j]))) {
+                order[i] = order[i - 1];
+                i--;
+            }
+            order[i] = j;
+        }
+        int np = 0;
+        int32_t prev = -1;
+        s_cpre[0] = 0;
+        for (int i = 0; i < nprobe; i++) {
+            const int32_t c = s_cell[order[i]];
+            if (c < 0 || c >= ncells || c == prev) continue;
+            prev = c;
+            const int64_t len = cell_start[c + 1] - cell_start[c];
+            s_r0[np] = cell_start[c];
+            s_len[np] = (int32_t)len;
+            s_cpre[np + 1] = s_cpre[np] + (int32_t)((len + 63) / 64);  // 64-key chunks
+            np++;
+        }
+        s_np = np;
+        count = 0;
+        s_tau = NONE;
+    }
+    if (tid < DW * 2 * 4) {
+        // Packed digits: dword ((dw*2 + h)*4 + p), nibble j = digit p of dim 16 dw + 2 j + h.
+        const int dw = tid >> 3, h = (tid >> 2) & 1, p = tid & 3;
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) word |= ((uint32_t)dig[p][16 * dw + 2 * j + h] & 15u) << (4 * j);
+        qpk[tid] = word;
+    }
+    __syncthreads();
+
+    const int quarter = lane & 3;
+    uint32_t qd[4][2][4];
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int p = 0; p < 4; p++) qd[v][h][p] = qpk[((4 * quarter + v) * 2 + h) * 4 + p];
+    const float qs = s_qs;
+    const int32_t sq = s_sq;
+    const int np = s_np;
+    const int32_t nchunks = s_cpre[np];
+    const int32_t c2_base = 9 * D;
+
+    // Wave w scans chunks w, w + 16, w + 32, ... of the query's cells taken in
+    // order (a chunk is 64 consecutive keys of one cell).  The chunk -> (cell,
+    // row) map is uniform per wave; lane l of sub-step s reads bytes 16*(l%4)..
+    // of key 16 s + l/4 of the chunk, so each load instruction of a wave reads
+    // 1 KB of consecutive codes.  Past a cell's end (or past the last chunk)
+    // lanes read the chunk's first key and are ignored.
+    int ccell = 0;  // cell of the chunk being fetched (chunks only move forward)
+    struct Chunk {
+        uint4 c[4];
+        float sc;
+        int64_t row0;
+        int32_t nk;
+    };
+    // Row of the first key of chunk 0 (the first non-empty cell): every read
+    // of a chunk past the end goes there, so no load ever leaves the store.
+    int32_t c0 = 0;
+    while (c0 < np - 1 && s_cpre[c0 + 1] == 0) c0++;
+    const int64_t safe_row0 = nchunks > 0 ? s_r0[c0] : 0;
+    auto fetch = [&](int32_t g, Chunk &ch) {
+        while (ccell < np - 1 && g >= s_cpre[ccell + 1]) ccell++;
+        const bool live = g < nchunks;
+        const int32_t key0 = (g - s_cpre[ccell]) * 64;
+        const int32_t nk = live ? min(64, s_len[ccell] - key0) : 0;
+        ch.row0 = live ? s_r0[ccell] + key0 : safe_row0;
+        ch.nk = nk;
+        const uint4 *cb = reinterpret_cast<const uint4 *>(codes + ch.row0 * (D / 4));
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int32_t kk = s * 16 + (lane >> 2);
+            ch.c[s] = cb[(kk < nk ? kk : 0) * 4 + quarter];
+        }
+        const int32_t ke = quarter * 16 + (lane >> 2);  // the key this lane scores
+        ch.sc = scales[ch.row0 + (ke < nk ? ke : 0)];
+    };
+    // Quad butterfly sum (lanes 4j..4j+3) with DPP row permutes.
+    auto quad_sum = [](int32_t x) {
+        x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+        x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+        return x;
+    };
+
+    // Each wave keeps its own candidate list (no workgroup barrier in the scan,
+    // so the 16 waves drift apart and hide each other's memory latency).  A
+    // wave's threshold is the 128th smallest key it has kept; the smallest of
+    // all waves' thresholds (shared through LDS) is also valid: the wave that
+    // owns it holds 128 keys at or below it.
+    uint64_t *wl = cand + wave * CAPW;
+    int wcount = 0;
+    uint64_t tau_w = NONE;
+    auto wave_compact = [&]() {
+        const int n = pow2_at_least(wcount);
+        for (int i = wcount + lane; i < n; i += 64) wl[i] = NONE;
+        wave_sort(wl, n, lane);
+        if (wcount >= KMAX) {
+            tau_w = wl[KMAX - 1];
+            atomicMin(reinterpret_cast<unsigned long long *>(&s_tau), (unsigned long long)tau_w);
+            wcount = KMAX;
+        }
+    };
+    auto score = [&](const Chunk &ch) {
+        int32_t duq[4], n12[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            int32_t acc[4] = {0, 0, 0, 0};
+            uint32_t nb = 0;
+            quarter_dot(ch.c[s], qd, acc, nb);
+            duq[s] = quad_sum(acc[0] + acc[1] * 16 + acc[2] * 256 + acc[3] * 4096);
+            n12[s] = quad_sum((int32_t)nb);
+        }
+        // Lane `quarter` of each quad scores the key of sub-step `quarter`.
+        const bool b0 = quarter & 1, b1 = quarter & 2;
+        const int32_t d = b1 ? (b0 ? duq[3] : duq[2]) : (b0 ? duq[1] : duq[0]);
+        const int32_t nn = b1 ? (b0 ? n12[3] : n12[2]) : (b0 ? n12[1] : n12[0]);
+        const int32_t ke = quarter * 16 + (lane >> 2);
+        const float sc = ch.sc;
+        const int32_t dot = 2 * d - 3 * sq;
+        const int32_t c2 = c2_base - 8 * nn;
+        const float t1 = (sc * sc) * 0.25f * (float)c2;
+        const float t3 = (sc * qs) * (float)dot;
+        const float dist = t1 - t3 + 0.0f;
+        const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)(ch.row0 + ke);
+        const uint64_t ts = __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint64_t tau = tau_w < ts ? tau_w : ts;
+        const bool take = ke < ch.nk && k64 < tau;
+        const uint64_t mask = __ballot(take);
+        if (take) {
+            const int pos = wcount + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            wl[pos] = k64;
+        }
+        wcount += __popcll(mask);
+        if (wcount > CAPW - 64 || (tau_w == NONE && wcount >= 256)) wave_compact();
+    };
+
+    // Two chunk buffers: while one is scored the other's loads are in flight.
+    // (Both halves run unconditionally: a chunk past the end has nk = 0 and
+    // scores nothing, and the loop body stays free of branches around loads.)
+    // The empty asm with a memory clobber pins each fetch's loads above the
+    // scoring that follows (the compiler would otherwise sink them to their
+    // first use); nothing reads the loaded registers there, so no wait is added.
+    Chunk ca, cb;
+    if (nchunks > 0) {  // uniform over the workgroup
+        // Phase A, in every wave: chunks wave and wave + 16 (2048 keys in all),
+        // every key kept.  One workgroup sort then gives the exact 128th
+        // smallest of them as the starting threshold of every wave; those 128
+        // stay in fin[0..128).
+        fetch(wave, ca);
+        fetch(wave + SW, cb);
+        asm volatile("" ::: "memory");
+        score(ca);
+        fetch(wave + 2 * SW, ca);
+        asm volatile("" ::: "memory");
+        score(cb);
+        __syncthreads();
+        for (int i = lane; i < wcount; i += 64) fin[atomicAdd(&count, 1)] = wl[i];
+        __syncthreads();
+        const int c0n = count;
+        const int n0 = pow2_at_least(c0n);
+        for (int i = c0n + tid; i < n0; i += STH) fin[i] = NONE;
+        __syncthreads();
+        bitonic_sort(fin, n0);
+        if (tid == 0) {
+            count = c0n < KMAX ? c0n : KMAX;
+            if (c0n >= KMAX) s_tau = fin[KMAX - 1];
+        }
+        wcount = 0;
+        __syncthreads();
+        // Phase B: the rest, two chunks per trip.
+        for (int32_t g = wave + 2 * SW; g < nchunks; g += 2 * SW) {
+            fetch(g + SW, cb);
+            asm volatile("" ::: "memory");
+            score(ca);
+            fetch(g + 2 * SW, ca);
+            asm volatile("" ::: "memory");
+            score(cb);
+        }
+    }
+    // Final: every wave sorts its list and keeps its best 128; the keys at or
+    // below the shared threshold (with the starting set, a superset of the
+    // query's top 128) are gathered behind the starting set and sorted.
+    wave_compact();
+    __syncthreads();
+    const uint64_t tfin = s_tau;
+    for (int i = lane; i < wcount; i += 64) {
+        const uint64_t e = wl[i];
+        if (e <= tfin) fin[atomicAdd(&count, 1)] = e;
+    }
+    __syncthreads();
     const int cnt = count;
     const int n = pow2_at_least(cnt);
-    for (int i = cnt + tid; i < n; i += 256) cand[i] = NONE;
+    for (int i = cnt + tid; i < n; i += STH) fin[i] = NONE;
     __syncthreads();
-    bitonic_sort(cand, n);
-    if (tid < KMAX) out[tid] = cand[tid];
-}
-
-// One workgroup per query: sort its nprobe lists, keep the k best, finalise.
-__global__ __launch_bounds__(256) void k_merge(const uint64_t *__restrict__ lists, int32_t nprobe,
-                                               const uint32_t *__restrict__ qpack, int32_t k,
-                                               int64_t *__restrict__ out_idx, float *__restrict__ out_dist) {
-    __shared__ uint64_t buf[PROBE_MAX * KMAX];
-    const int64_t q = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int total = nprobe * KMAX;
-    int n = KMAX;
-    while (n < total) n <<= 1;
-    const uint64_t *src = lists + q * (int64_t)total;
-    for (int i = tid; i < n; i += 256) buf[i] = i < total ? src[i] : NONE;
-    __syncthreads();
-    bitonic_sort(buf, n);
-    const float qn = reinterpret_cast<const QScalars *>(qpack + q * QPACK + 128)->qn;
-    for (int j = tid; j < k; j += 256) {
-        const uint64_t e = buf[j];
+    bitonic_sort(fin, n);
+    const float qn = s_qn;
+    for (int j = tid; j < k; j += STH) {
+        const uint64_t e = fin[j];
         if (e == NONE) {
             out_idx[q * k + j] = -1;
             out_dist[q * k + j] = __builtin_inff();
@@ -422,22 +573,10 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     if ((reinterpret_cast<uintptr_t>(codes) & 15) != 0 || (reinterpret_cast<uintptr_t>(queries) & 15) != 0)
         return st::fail(ST_ERR_INVALID, "search_ivf: codes and queries must be 16-byte aligned");
     if (nq == 0) return ST_OK;
-    if (nq * nprobe > INT32_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many queries for one call");
+    if (nq > INT32_MAX / PROBE_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many queries for one call");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
-    const size_t qbytes = (size_t)nq * QPACK * 4;
-    const size_t lbytes = (size_t)nq * nprobe * KMAX * 8;
-    uint8_t *ws = static_cast<uint8_t *>(st::scratch(st::SCRATCH_KNN, qbytes + lbytes));
-    if (!ws) return ST_ERR_OOM;
-    uint32_t *qpack = reinterpret_cast<uint32_t *>(ws);
-    uint64_t *lists = reinterpret_cast<uint64_t *>(ws + qbytes);
-    hipStream_t s = st::stream_of(stream);
-    hipLaunchKernelGGL(k_prep, dim3((unsigned)nq), dim3(64), 0, s, queries, qpack);
-    ST_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_scan, dim3((unsigned)(nq * nprobe)), dim3(256), 0, s, codes, scales, cell_start, ncells,
-                       probes, (int32_t)nprobe, qpack, lists);
-    ST_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)nq), dim3(256), 0, s, lists, (int32_t)nprobe, qpack, (int32_t)k,
-                       out_idx, out_dist);
+    hipLaunchKernelGGL(k_search, dim3((unsigned)nq), dim3(STH), 0, st::stream_of(stream), codes, scales, cell_start,
+                       ncells, queries, probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist);
     ST_LAUNCH_CHECK();
     return ST_OK;
 }
