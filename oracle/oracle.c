@@ -348,7 +348,7 @@ void orc_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t *codes, 
 /*                                                                            */
 /* Query q (f32, d) -> power-of-two scale qs = 2^(E-14) where M = max|q_i| = */
 /* m * 2^E, m in [0.5, 1) (qs = 1 when M == 0); Q_i = clamp(rint(q_i / qs),  */
-/* -16384, 16384) (exact: qs is a power of two).  Key code u_i in 0..3 and   */
+/* -16384, 16383) (exact: qs is a power of two).  Key code u_i in 0..3 and   */
 /* scale s decode to k_i = (u_i - 1.5) s = c_i s / 2 with c_i = 2u_i - 3.     */
 /*   dot  = sum c_i Q_i                (exact int32)                          */
 /*   c2   = sum c_i^2 = 256-ish..      (exact int32)                          */
@@ -382,7 +382,7 @@ void orc_knn_prep_query(const float *q, int64_t d, int16_t *Q, orc_qprep *prep) 
     int32_t sq = 0;
     for (int64_t i = 0; i < d; i++) {
         float v = rintf(q[i] / qs);
-        if (v > 16384.0f) v = 16384.0f;
+        if (v > 16383.0f) v = 16383.0f;
         if (v < -16384.0f) v = -16384.0f;
         int32_t x = (int32_t)v;
         Q[i] = (int16_t)x;

@@ -195,23 +195,17 @@ __device__ __forceinline__ int pow2_at_least(int x) {
     return n;
 }
 
-// One lane's quarter of a key (code dwords 4*quarter .. +3) against the
-// query's balanced base-16 digits: acc[p] gathers sum u*digit_p over the
-// quarter, n12 the codes with u in {1, 2}.
-__device__ __forceinline__ void quarter_dot(const uint4 &c, const uint32_t (&qd)[4][2][4], int32_t (&acc)[4],
-                                            uint32_t &n12) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const uint32_t ea = w[v] & 0x33333333u;         // nibble j: code 2j
-        const uint32_t eb = (w[v] >> 2) & 0x33333333u;  // nibble j: code 2j + 1
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            acc[p] = __builtin_amdgcn_sdot8((int)ea, (int)qd[v][0][p], acc[p], false);
-            acc[p] = __builtin_amdgcn_sdot8((int)eb, (int)qd[v][1][p], acc[p], false);
-        }
-        n12 += __popc((w[v] ^ (w[v] >> 1)) & 0x55555555u);
-    }
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Sum over the four 16-lane rows of a wave (every lane gets its column's sum),
+// with the gfx950 row swaps: x + swap16(x), then + swap32.
+__device__ __forceinline__ int32_t rows_sum(int32_t x) {
+    auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    x = (int32_t)(a[0] + a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return (int32_t)(b[0] + b[1]);
 }
 
 // grid: one workgroup of 1024 threads per query.
@@ -223,8 +217,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     __shared__ uint64_t cand[SW * CAPW];  // per-wave candidate lists
     __shared__ uint64_t fin[FIN];         // the starting set and the final gather
     __shared__ uint64_t s_tau;            // min over the waves' thresholds
-    __shared__ int8_t dig[4][D];
-    __shared__ uint32_t qpk[DW * 2 * 4];
+    __shared__ int16_t s_Q[D];
     __shared__ float s_qs, s_qn;
     __shared__ int32_t s_sq, s_np, count;
     __shared__ int32_t s_cell[PROBE_MAX], s_share[PROBE_MAX];
@@ -235,8 +228,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     const int64_t q = blockIdx.x;
 
     if (wave == 0) {
-        // Query quantisation: qs = 2^(E-14) with max|q| = m 2^E, Q = clamp(rint(q / qs), +-16384),
-        // then balanced base-16 digits d0..d3 in [-8, 7] with Q = d0 + 16 d1 + 256 d2 + 4096 d3.
+        // Query quantisation: qs = 2^(E-14) with max|q| = m 2^E, Q = clamp(rint(q / qs), -16384, 16383).
         const float4 v = reinterpret_cast<const float4 *>(queries + q * D)[lane];
         const float x[4] = {v.x, v.y, v.z, v.w};
         const float mx = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
@@ -251,16 +243,10 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         double sq2 = 0.0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const float r = fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16384.f);
-            int32_t Q = (int32_t)r;
+            const int32_t Q = (int32_t)fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16383.f);
             sq += Q;
             sq2 += (double)Q * (double)Q;
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const int32_t d = p < 3 ? ((Q + 8) & 15) - 8 : Q;
-                dig[p][4 * lane + t] = (int8_t)d;
-                Q = (Q - d) >> 4;
-            }
+            s_Q[4 * lane + t] = (int16_t)Q;
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
@@ -290,7 +276,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     if (tid == 0) {
         // Cells scanned by several queries of the batch first (their bytes are
         // then read while still in the MALL), a repeated cell once, invalid ids
-        // skipped; s_pre holds the running key count.
+        // skipped; s_cpre counts 64-key chunks.
         int order[PROBE_MAX];
         for (int j = 0; j < nprobe; j++) {
             int i = j;
@@ -311,52 +297,79 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             const int64_t len = cell_start[c + 1] - cell_start[c];
             s_r0[np] = cell_start[c];
             s_len[np] = (int32_t)len;
-            s_cpre[np + 1] = s_cpre[np] + (int32_t)((len + 63) / 64);  // 64-key chunks
+            s_cpre[np + 1] = s_cpre[np] + (int32_t)((len + 63) / 64);
             np++;
         }
         s_np = np;
         count = 0;
         s_tau = NONE;
     }
-    if (tid < DW * 2 * 4) {
-        // Packed digits: dword ((dw*2 + h)*4 + p), nibble j = digit p of dim 16 dw + 2 j + h.
-        const int dw = tid >> 3, h = (tid >> 2) & 1, p = tid & 3;
-        uint32_t word = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) word |= ((uint32_t)dig[p][16 * dw + 2 * j + h] & 15u) << (4 * j);
-        qpk[tid] = word;
-    }
     __syncthreads();
 
-    const int quarter = lane & 3;
-    uint32_t qd[4][2][4];
+    // Matrix-core operands.  The key side (B, 128 x 16 per k-step, FP4 e2m1):
+    // a code u kept in the low two bits of a nibble is the e2m1 number u / 2
+    // (0, 0.5, 1, 1.5), so w & 0x33333333 and (w >> 2) & 0x33333333 are ready
+    // operands: nibble j of the first is code 2j of code dword w, of the
+    // second code 2j + 1.  Lane l supplies column l % 16 (a key) and the 32
+    // values of k-block l / 16; at k-step m (0, 1) they are dims
+    // 16 (4 (l/16) + 2m) + [0, 2, .., 14], then + 1, then the same for code
+    // dword 4 (l/16) + 2m + 1: FP4 nibble n of k-block h is k = 32 h + n.  The
+    // query side (A, FP8 e4m3) orders k differently: byte n of lane group g is
+    // k = 16 g + n for n < 16 and k = 64 + 16 g + (n - 16) above.  Row p < 4
+    // holds balanced base-16 digit p of Q (Q = d0 + 16 d1 + 256 d2 + 4096 d3,
+    // d in [-8, 7], exact in FP8) at the dim its k pairs with; rows 4..15 are
+    // zero.  Products and sums are small half-integers, exact in the f32
+    // accumulator.
+    const int row = lane >> 4, col = lane & 15;
+    v8i aq[2];
 #pragma unroll
-    for (int v = 0; v < 4; v++)
+    for (int m = 0; m < 2; m++) {
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+        for (int v = 0; v < 8; v++) {
+            // elements 4v .. 4v + 3 of this lane's 32
+            float f[4];
 #pragma unroll
-            for (int p = 0; p < 4; p++) qd[v][h][p] = qpk[((4 * quarter + v) * 2 + h) * 4 + p];
+            for (int e = 0; e < 4; e++) {
+                const int n = 4 * v + e;
+                const int k = n < 16 ? 16 * row + n : 64 + 16 * row + (n - 16);
+                const int nb = k & 31;
+                const int dword = 4 * (k >> 5) + 2 * m + (nb >> 4);
+                const int code = 2 * (nb & 7) + ((nb >> 3) & 1);
+                int32_t Q = s_Q[16 * dword + code];
+                int32_t dgt = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int32_t d = p < 3 ? ((Q + 8) & 15) - 8 : Q;
+                    if (p == col) dgt = d;
+                    Q = (Q - d) >> 4;
+                }
+                f[e] = col < 4 ? (float)dgt : 0.f;
+            }
+            int32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+            word = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], word, true);
+            aq[m][v] = word;
+        }
+    }
     const float qs = s_qs;
     const int32_t sq = s_sq;
     const int np = s_np;
     const int32_t nchunks = s_cpre[np];
     const int32_t c2_base = 9 * D;
 
-    // Wave w scans chunks w, w + 16, w + 32, ... of the query's cells taken in
-    // order (a chunk is 64 consecutive keys of one cell).  The chunk -> (cell,
-    // row) map is uniform per wave; lane l of sub-step s reads bytes 16*(l%4)..
-    // of key 16 s + l/4 of the chunk, so each load instruction of a wave reads
-    // 1 KB of consecutive codes.  Past a cell's end (or past the last chunk)
-    // lanes read the chunk's first key and are ignored.
-    int ccell = 0;  // cell of the chunk being fetched (chunks only move forward)
+    // Wave w scans chunks w, w + 16, ... of the query's cells taken in order (a
+    // chunk is 64 consecutive keys of one cell; the chunk -> (cell, row) map is
+    // uniform per wave).  For group G (keys 16G..16G+15 of the chunk) lane l
+    // loads bytes 16 (l/16) .. of key 16G + l%16: the 16-byte key operand of
+    // matrix-core column l%16, k-block l/16, for the four k-steps; a wave's
+    // load reads 1 KB of consecutive codes.  Past a cell's end (or the last
+    // chunk) lanes read the chunk's first key and are ignored.
+    int ccell = 0;
     struct Chunk {
         uint4 c[4];
         float sc;
         int64_t row0;
         int32_t nk;
     };
-    // Row of the first key of chunk 0 (the first non-empty cell): every read
-    // of a chunk past the end goes there, so no load ever leaves the store.
     int32_t c0 = 0;
     while (c0 < np - 1 && s_cpre[c0 + 1] == 0) c0++;
     const int64_t safe_row0 = nchunks > 0 ? s_r0[c0] : 0;
@@ -369,18 +382,11 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         ch.nk = nk;
         const uint4 *cb = reinterpret_cast<const uint4 *>(codes + ch.row0 * (D / 4));
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int32_t kk = s * 16 + (lane >> 2);
-            ch.c[s] = cb[(kk < nk ? kk : 0) * 4 + quarter];
+        for (int G = 0; G < 4; G++) {
+            const int32_t kk = 16 * G + col;
+            ch.c[G] = cb[(kk < nk ? kk : 0) * 4 + row];
         }
-        const int32_t ke = quarter * 16 + (lane >> 2);  // the key this lane scores
-        ch.sc = scales[ch.row0 + (ke < nk ? ke : 0)];
-    };
-    // Quad butterfly sum (lanes 4j..4j+3) with DPP row permutes.
-    auto quad_sum = [](int32_t x) {
-        x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-        x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-        return x;
+        ch.sc = scales[ch.row0 + (lane < nk ? lane : 0)];  // lane l scores chunk key l
     };
 
     // Each wave keeps its own candidate list (no workgroup barrier in the scan,
@@ -402,30 +408,48 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         }
     };
     auto score = [&](const Chunk &ch) {
-        int32_t duq[4], n12[4];
+        int32_t vg[4];
+        int32_t n12 = 0;
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            int32_t acc[4] = {0, 0, 0, 0};
-            uint32_t nb = 0;
-            quarter_dot(ch.c[s], qd, acc, nb);
-            duq[s] = quad_sum(acc[0] + acc[1] * 16 + acc[2] * 256 + acc[3] * 4096);
-            n12[s] = quad_sum((int32_t)nb);
+        for (int G = 0; G < 4; G++) {
+            const uint32_t w[4] = {ch.c[G].x, ch.c[G].y, ch.c[G].z, ch.c[G].w};
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const v8i bk = {(int32_t)(w[2 * m] & 0x33333333u), (int32_t)((w[2 * m] >> 2) & 0x33333333u),
+                                (int32_t)(w[2 * m + 1] & 0x33333333u), (int32_t)((w[2 * m + 1] >> 2) & 0x33333333u),
+                                0, 0, 0, 0};
+                // A: FP8 e4m3 (cbsz 0), B: FP4 e2m1 (blgp 4), unit block scales (E8M0 127).
+                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aq[m], bk, acc, 0, 4, 0, 127, 0, 127);
+            }
+            // Rows 0..3 (registers 0..3 of row-0 lanes) hold sum (u/2) d_p: sum u Q = 2 sum_p 16^p D[p].
+            const float dq = 2.f * (acc[0] + 16.f * (acc[1] + 16.f * (acc[2] + 16.f * acc[3])));
+            vg[G] = (int32_t)dq;
+            // Codes with u in {1, 2} of key 16G + col over this lane's 64 dims, summed over the 4 rows.
+            int32_t p = 0;
+#pragma unroll
+            for (int s = 0; s < 4; s++) p += __popc((w[s] ^ (w[s] >> 1)) & 0x55555555u);
+            p = rows_sum(p);
+            n12 = row == G ? p : n12;
         }
-        // Lane `quarter` of each quad scores the key of sub-step `quarter`.
-        const bool b0 = quarter & 1, b1 = quarter & 2;
-        const int32_t d = b1 ? (b0 ? duq[3] : duq[2]) : (b0 ? duq[1] : duq[0]);
-        const int32_t nn = b1 ? (b0 ? n12[3] : n12[2]) : (b0 ? n12[1] : n12[0]);
-        const int32_t ke = quarter * 16 + (lane >> 2);
+        // Route group G's dot (valid in row 0) to row G: lane l ends with key l's.
+        {
+            auto a = __builtin_amdgcn_permlane32_swap((unsigned)vg[0], (unsigned)vg[2], false, false);
+            auto b = __builtin_amdgcn_permlane32_swap((unsigned)vg[1], (unsigned)vg[3], false, false);
+            auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+            vg[0] = (int32_t)c[0];
+        }
+        const int32_t duq = vg[0];
         const float sc = ch.sc;
-        const int32_t dot = 2 * d - 3 * sq;
-        const int32_t c2 = c2_base - 8 * nn;
+        const int32_t dot = 2 * duq - 3 * sq;
+        const int32_t c2 = c2_base - 8 * n12;
         const float t1 = (sc * sc) * 0.25f * (float)c2;
         const float t3 = (sc * qs) * (float)dot;
         const float dist = t1 - t3 + 0.0f;
-        const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)(ch.row0 + ke);
+        const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)(ch.row0 + lane);
         const uint64_t ts = __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const uint64_t tau = tau_w < ts ? tau_w : ts;
-        const bool take = ke < ch.nk && k64 < tau;
+        const bool take = lane < ch.nk && k64 < tau;
         const uint64_t mask = __ballot(take);
         if (take) {
             const int pos = wcount + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
@@ -436,7 +460,6 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         if (wcount > CAPW - 64 || (tau_w == NONE && wcount >= 256)) wave_compact();
     };
 
-    // Two chunk buffers: while one is scored the other's loads are in flight.
     // (Both halves run unconditionally: a chunk past the end has nk = 0 and
     // scores nothing, and the loop body stays free of branches around loads.)
     // The empty asm with a memory clobber pins each fetch's loads above the

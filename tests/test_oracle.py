@@ -365,7 +365,7 @@ def test_query_quantisation_is_exact_power_of_two_scaling():
         Q, prep = oracle.knn_prep_query(q)
         qs = prep.qs
         assert math.frexp(qs)[0] == 0.5  # power of two
-        assert 8192 <= np.abs(Q.astype(np.int64)).max() <= 16384
+        assert 8192 <= np.abs(Q.astype(np.int64)).max() <= 16384 and Q.max() <= 16383
         assert np.all(np.abs(Q.astype(np.float64) * qs - q.astype(np.float64)) <= qs / 2)
         assert prep.sq == int(Q.astype(np.int64).sum())
         assert prep.qn == np.float32(float((Q.astype(np.int64) ** 2).sum())) * np.float32(qs * qs)
