@@ -19,27 +19,25 @@
 // oracle reproduces bit for bit.  Ranking is by (dist, key index) ascending.
 //
 // Search design: one 1024-thread workgroup (16 wave64s) per query streams the
-// concatenation of its probed cells, 1024 keys (64 KB of codes) per iteration
-// with the next iteration's loads in flight.  Lane l handles bytes 16*(l%4)..
-// of a key (4 of its 16 code dwords), so a wave's loads are fully coalesced
-// 1 KB rows and each lane keeps only its quarter of the query in registers.
-// The query is held as balanced base-16 digits (Q = d0 + 16 d1 + 256 d2 +
-// 4096 d3, d in [-8, 7]); per code dword two masks give the codes as 4-bit
-// nibbles and eight v_dot8_i32_i4 (one per digit and nibble set) accumulate
-// the exact dot, one popcount gives c2.  The four quarter sums are combined
-// with two butterfly shuffles (integers: exact in any order).
+// concatenation of its probed cells in 64-key chunks, each wave with three
+// chunks in flight.  Scoring runs on the matrix cores: the key codes are FP4
+// e2m1 operands as stored (a 2-bit code in the low bits of a nibble is u / 2),
+// the query is four FP8 rows of balanced base-16 digits, and one scaled
+// FP8 x FP4 MFMA per 128 dims gives the exact integer dot of 16 keys; one
+// popcount per code dword gives c2.
 //
 // Top-k: each wave appends candidates with key64 = (ordered dist bits << 32 |
-// index) below its threshold to its own LDS list (ballot + mbcnt, no atomics,
-// no workgroup barrier in the scan); when the list fills (or after the first
-// 256 candidates) a wave-level bitonic sort keeps its 128 smallest and its
-// threshold becomes the 128th, published to the workgroup through an LDS
-// atomicMin.  Only keys with at least 128 smaller keys already seen are
-// dropped, so the exact top-128 survives whatever the order, and the final
-// sort makes the result deterministic.  Cells that other queries of the
-// batch also probe are scanned first, so their bytes are read while the other
-// workgroups still find them in the MALL.
+// index) below the shared threshold to its own LDS list (ballot + mbcnt, no
+// atomics, no workgroup barrier in the scan); when the list holds 192 a
+// wave-level bitonic sort keeps its 128 smallest, publishes its 8th smallest,
+// and the threshold drops to the smaller of its 128th and the largest of the
+// 16 waves' 8th smallest (either has 128 keys at or below it).  Only keys with
+// at least 128 smaller keys are dropped, so the exact top-128 survives
+// whatever the order; the output position of each survivor is its rank.
+// Cells that other queries of the batch also probe are scanned first, so
+// their bytes are read while the other workgroups still find them in the MALL.
 #include <cstring>
+#include <type_traits>
 
 #include "common.h"
 
@@ -50,8 +48,7 @@ namespace {
 constexpr int D = 256;          // key width handled by the scan
 constexpr int DW = D / 16;      // code dwords per key
 constexpr int KMAX = 128;       // neighbours kept per query (knn.rs:21)
-constexpr int CAPW = 512;       // LDS candidate list per wave (entries)
-constexpr int FIN = 4096;       // LDS starting set + final gather (entries)
+constexpr int CAPW = 256;       // LDS candidate list per wave (entries)
 constexpr int PROBE_MAX = 16;   // most cells one query probes (ivf.rs:126)
 constexpr uint64_t NONE = ~0ull;
 
@@ -137,33 +134,11 @@ __global__ __launch_bounds__(256) void k_synth_keys(uint64_t seed, int64_t row0,
 
 constexpr int SW = 16;          // waves per search workgroup
 constexpr int STH = SW * 64;    // threads per search workgroup (one workgroup per query)
-constexpr int KPI = STH;        // keys scanned per iteration: 4 lanes per key, 4 sub-steps
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
-}
-
-// Sorts buf[0..n) ascending (n a power of two) with all threads of the block.
-__device__ void bitonic_sort(uint64_t *buf, int n) {
-    const int tid = threadIdx.x, nt = blockDim.x;
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < n; i += nt) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = buf[i], b = buf[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((a > b) == up) {
-                        buf[i] = b;
-                        buf[ixj] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
 }
 
 // Sorts buf[0..n) ascending (n a power of two) within one wave: LDS operations
@@ -195,18 +170,20 @@ __device__ __forceinline__ int pow2_at_least(int x) {
     return n;
 }
 
-typedef int32_t v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
 typedef int32_t v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Sum over the four 16-lane rows of a wave (every lane gets its column's sum),
-// with the gfx950 row swaps: x + swap16(x), then + swap32.
-__device__ __forceinline__ int32_t rows_sum(int32_t x) {
-    auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-    x = (int32_t)(a[0] + a[1]);
-    auto b = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-    return (int32_t)(b[0] + b[1]);
-}
+constexpr int E8 = KMAX / SW;  // each wave's published rank: SW * E8 = KMAX keys
 
 // grid: one workgroup of 1024 threads per query.
 __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const float *scales,
@@ -215,13 +192,15 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
                                                 int32_t nq, int32_t nprobe, int32_t k, int64_t *__restrict__ out_idx,
                                                 float *__restrict__ out_dist) {
     __shared__ uint64_t cand[SW * CAPW];  // per-wave candidate lists
-    __shared__ uint64_t fin[FIN];         // the starting set and the final gather
-    __shared__ uint64_t s_tau;            // min over the waves' thresholds
+    __shared__ uint64_t fin[SW * KMAX];   // the final gather
+    __shared__ uint64_t s_tau;            // shared threshold (only decreases)
+    __shared__ uint64_t s_e8[SW];         // each wave's E8-th smallest kept key
     __shared__ int16_t s_Q[D];
     __shared__ float s_qs, s_qn;
     __shared__ int32_t s_sq, s_np, count;
     __shared__ int32_t s_cell[PROBE_MAX], s_share[PROBE_MAX];
-    __shared__ int64_t s_r0[PROBE_MAX];
+    __shared__ int64_t s_c0[PROBE_MAX], s_c1[PROBE_MAX];
+    __shared__ int64_t s_r0[PROBE_MAX], s_nrows;
     __shared__ int32_t s_len[PROBE_MAX], s_cpre[PROBE_MAX + 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -258,18 +237,33 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             s_qn = (float)sq2 * (qs * qs);
             s_sq = sq;
         }
-    } else {
-        // How many (query, probe) pairs of the whole batch scan each probed cell.
-        for (int j = wave - 1; j < nprobe; j += SW - 1) {
-            const int32_t cell = probes[q * nprobe + j];
-            int cnt = 0;
-            for (int64_t i = lane; i < (int64_t)nq * nprobe; i += 64) cnt += probes[i] == cell;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
-            if (lane == 0) {
-                s_cell[j] = cell;
-                s_share[j] = cnt;
-            }
+    } else if (wave == 1) {
+        // The probed cells and their row ranges (all loads in flight together);
+        // an id outside [0, ncells) is recorded as -1 and skipped.
+        if (lane < nprobe) {
+            const int32_t c = probes[q * nprobe + lane];
+            const bool ok = c >= 0 && c < ncells;
+            s_cell[lane] = ok ? c : -1;
+            s_share[lane] = 0;
+            s_c0[lane] = ok ? cell_start[c] : 0;
+            s_c1[lane] = ok ? cell_start[c + 1] : 0;
+        }
+        if (lane == 63) s_nrows = cell_start[ncells];
+    } else if (wave == 2) {
+        if (lane < SW) s_e8[lane] = NONE;
+        if (lane == 0) {
+            s_tau = NONE;
+            count = 0;
+        }
+    }
+    __syncthreads();
+    // How many (query, probe) pairs of the whole batch scan each probed cell.
+    {
+        const int64_t total = (int64_t)nq * nprobe;
+        for (int64_t i = tid; i < total; i += STH) {
+            const int32_t v = probes[i];
+            for (int j = 0; j < nprobe; j++)
+                if (v == s_cell[j]) atomicAdd(&s_share[j], 1);
         }
     }
     __syncthreads();
@@ -291,18 +285,17 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         int32_t prev = -1;
         s_cpre[0] = 0;
         for (int i = 0; i < nprobe; i++) {
-            const int32_t c = s_cell[order[i]];
-            if (c < 0 || c >= ncells || c == prev) continue;
+            const int j = order[i];
+            const int32_t c = s_cell[j];
+            if (c < 0 || c == prev) continue;
             prev = c;
-            const int64_t len = cell_start[c + 1] - cell_start[c];
-            s_r0[np] = cell_start[c];
+            const int64_t len = s_c1[j] - s_c0[j];
+            s_r0[np] = s_c0[j];
             s_len[np] = (int32_t)len;
             s_cpre[np + 1] = s_cpre[np] + (int32_t)((len + 63) / 64);
             np++;
         }
         s_np = np;
-        count = 0;
-        s_tau = NONE;
     }
     __syncthreads();
 
@@ -316,10 +309,10 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     // dword 4 (l/16) + 2m + 1: FP4 nibble n of k-block h is k = 32 h + n.  The
     // query side (A, FP8 e4m3) orders k differently: byte n of lane group g is
     // k = 16 g + n for n < 16 and k = 64 + 16 g + (n - 16) above.  Row p < 4
-    // holds balanced base-16 digit p of Q (Q = d0 + 16 d1 + 256 d2 + 4096 d3,
-    // d in [-8, 7], exact in FP8) at the dim its k pairs with; rows 4..15 are
-    // zero.  Products and sums are small half-integers, exact in the f32
-    // accumulator.
+    // holds twice the balanced base-16 digit p of Q (Q = d0 + 16 d1 + 256 d2 +
+    // 4096 d3, d0..d2 in [-8, 7], d3 in [-4, 4]; 2d is exact in FP8) at the dim
+    // its k pairs with; rows 4..15 are zero.  Row p of the product is then the
+    // integer sum_i d_p,i u_i, exact in the f32 accumulator.
     const int row = lane >> 4, col = lane & 15;
     v8i aq[2];
 #pragma unroll
@@ -343,7 +336,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
                     if (p == col) dgt = d;
                     Q = (Q - d) >> 4;
                 }
-                f[e] = col < 4 ? (float)dgt : 0.f;
+                f[e] = col < 4 ? (float)(2 * dgt) : 0.f;
             }
             int32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
             word = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], word, true);
@@ -354,62 +347,86 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     const int32_t sq = s_sq;
     const int np = s_np;
     const int32_t nchunks = s_cpre[np];
+    const int64_t nrows = s_nrows;
     const int32_t c2_base = 9 * D;
 
     // Wave w scans chunks w, w + 16, ... of the query's cells taken in order (a
-    // chunk is 64 consecutive keys of one cell; the chunk -> (cell, row) map is
-    // uniform per wave).  For group G (keys 16G..16G+15 of the chunk) lane l
-    // loads bytes 16 (l/16) .. of key 16G + l%16: the 16-byte key operand of
-    // matrix-core column l%16, k-block l/16, for the four k-steps; a wave's
-    // load reads 1 KB of consecutive codes.  Past a cell's end (or the last
-    // chunk) lanes read the chunk's first key and are ignored.
+    // chunk is the up to 64 keys of one cell at rows row0 .. row0 + nk; the
+    // chunk -> (cell, row) map is uniform per wave).  A chunk is read as the 64
+    // keys from base = min(row0, nrows - 64), so the loads of a chunk are four
+    // fixed offsets from one address and never leave the store; lane l scores
+    // key base + l and keeps it when lo <= l < hi.  For group G (keys 16G ..
+    // 16G + 15 of the 64) lane l loads bytes 16 (l/16) .. of key 16G + l%16:
+    // the 16-byte key operand of matrix-core column l%16, k-block l/16, for the
+    // four k-steps; a wave's load reads 1 KB of consecutive codes.  A store of
+    // fewer than 64 keys (SMALL) is read from base 0 with each key index
+    // clamped to the store.
     int ccell = 0;
     struct Chunk {
         uint4 c[4];
         float sc;
-        int64_t row0;
-        int32_t nk;
+        int64_t base;
+        int32_t lo, hi;
     };
     int32_t c0 = 0;
     while (c0 < np - 1 && s_cpre[c0 + 1] == 0) c0++;
     const int64_t safe_row0 = nchunks > 0 ? s_r0[c0] : 0;
-    auto fetch = [&](int32_t g, Chunk &ch) {
+    auto fetch = [&](auto small, int32_t g, Chunk &ch) {
+        constexpr bool SMALL = decltype(small)::value;
         while (ccell < np - 1 && g >= s_cpre[ccell + 1]) ccell++;
         const bool live = g < nchunks;
         const int32_t key0 = (g - s_cpre[ccell]) * 64;
         const int32_t nk = live ? min(64, s_len[ccell] - key0) : 0;
-        ch.row0 = live ? s_r0[ccell] + key0 : safe_row0;
-        ch.nk = nk;
-        const uint4 *cb = reinterpret_cast<const uint4 *>(codes + ch.row0 * (D / 4));
+        const int64_t row0 = live ? s_r0[ccell] + key0 : safe_row0;
+        const int64_t base = SMALL ? 0 : (row0 < nrows - 64 ? row0 : nrows - 64);
+        ch.base = base;
+        ch.lo = (int32_t)(row0 - base);
+        ch.hi = ch.lo + nk;
+        const uint4 *cb = reinterpret_cast<const uint4 *>(codes + base * (D / 4));
 #pragma unroll
         for (int G = 0; G < 4; G++) {
-            const int32_t kk = 16 * G + col;
-            ch.c[G] = cb[(kk < nk ? kk : 0) * 4 + row];
+            int32_t kk = 16 * G + col;
+            if (SMALL) kk = kk < nrows ? kk : 0;
+            ch.c[G] = cb[kk * 4 + row];
         }
-        ch.sc = scales[ch.row0 + (lane < nk ? lane : 0)];  // lane l scores chunk key l
+        ch.sc = scales[base + (SMALL ? (lane < nrows ? lane : 0) : lane)];  // lane l scores key base + l
     };
 
     // Each wave keeps its own candidate list (no workgroup barrier in the scan,
-    // so the 16 waves drift apart and hide each other's memory latency).  A
-    // wave's threshold is the 128th smallest key it has kept; the smallest of
-    // all waves' thresholds (shared through LDS) is also valid: the wave that
-    // owns it holds 128 keys at or below it.
+    // so the 16 waves drift apart and hide each other's memory latency).  Any
+    // key above a threshold t with at least 128 scored keys at or below it can
+    // be dropped.  Two such thresholds are kept: the wave's own 128th smallest
+    // key, and the largest of the waves' published E8-th smallest keys (16
+    // waves x 8 keys at or below it).  Their minimum over the workgroup lives
+    // in s_tau, which only decreases.
     uint64_t *wl = cand + wave * CAPW;
     int wcount = 0;
     uint64_t tau_w = NONE;
+    // Folds this wave's thresholds into s_tau and drops the (sorted) list's
+    // keys above the result.
+    auto refresh = [&]() {
+        const uint64_t m = wave_max_u64(lane < SW ? s_e8[lane] : 0ull);
+        const uint64_t t = tau_w < m ? tau_w : m;
+        if (lane == 0) atomicMin(reinterpret_cast<unsigned long long *>(&s_tau), (unsigned long long)t);
+        const uint64_t ts = __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint64_t cut = t < ts ? t : ts;
+        int c = 0;
+        for (int i = 0; i < wcount; i += 64) c += __popcll(__ballot(i + lane < wcount && wl[i + lane] <= cut));
+        wcount = c;
+    };
     auto wave_compact = [&]() {
         const int n = pow2_at_least(wcount);
         for (int i = wcount + lane; i < n; i += 64) wl[i] = NONE;
         wave_sort(wl, n, lane);
         if (wcount >= KMAX) {
             tau_w = wl[KMAX - 1];
-            atomicMin(reinterpret_cast<unsigned long long *>(&s_tau), (unsigned long long)tau_w);
             wcount = KMAX;
         }
+        if (wcount >= E8 && lane == 0) s_e8[wave] = wl[E8 - 1];
+        refresh();
     };
     auto score = [&](const Chunk &ch) {
-        int32_t vg[4];
-        int32_t n12 = 0;
+        int32_t vg[4], pc[4];
 #pragma unroll
         for (int G = 0; G < 4; G++) {
             const uint32_t w[4] = {ch.c[G].x, ch.c[G].y, ch.c[G].z, ch.c[G].w};
@@ -422,34 +439,40 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
                 // A: FP8 e4m3 (cbsz 0), B: FP4 e2m1 (blgp 4), unit block scales (E8M0 127).
                 acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aq[m], bk, acc, 0, 4, 0, 127, 0, 127);
             }
-            // Rows 0..3 (registers 0..3 of row-0 lanes) hold sum (u/2) d_p: sum u Q = 2 sum_p 16^p D[p].
-            const float dq = 2.f * (acc[0] + 16.f * (acc[1] + 16.f * (acc[2] + 16.f * acc[3])));
+            // Rows 0..3 (registers 0..3 of row-0 lanes, zero in other lanes) hold
+            // sum d_p u; sum u Q = sum_p 16^p (row p), every step an exact integer.
+            const float dq = __builtin_fmaf(16.f, __builtin_fmaf(16.f, __builtin_fmaf(16.f, acc[3], acc[2]), acc[1]),
+                                            acc[0]);
             vg[G] = (int32_t)dq;
-            // Codes with u in {1, 2} of key 16G + col over this lane's 64 dims, summed over the 4 rows.
+            // Codes with u in {1, 2} of key 16G + col among this lane's 64 dims.
             int32_t p = 0;
 #pragma unroll
             for (int s = 0; s < 4; s++) p += __popc((w[s] ^ (w[s] >> 1)) & 0x55555555u);
-            p = rows_sum(p);
-            n12 = row == G ? p : n12;
+            pc[G] = p;
         }
-        // Route group G's dot (valid in row 0) to row G: lane l ends with key l's.
+        // Route group G's dot (in row 0) to row G and sum group G's counts over
+        // the four rows into row G: lane l ends with key l's dot and count.
+        int32_t duq, n12;
         {
             auto a = __builtin_amdgcn_permlane32_swap((unsigned)vg[0], (unsigned)vg[2], false, false);
             auto b = __builtin_amdgcn_permlane32_swap((unsigned)vg[1], (unsigned)vg[3], false, false);
             auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-            vg[0] = (int32_t)c[0];
+            duq = (int32_t)c[0];
+            auto x = __builtin_amdgcn_permlane32_swap((unsigned)pc[0], (unsigned)pc[2], false, false);
+            auto y = __builtin_amdgcn_permlane32_swap((unsigned)pc[1], (unsigned)pc[3], false, false);
+            auto z = __builtin_amdgcn_permlane16_swap(x[0] + x[1], y[0] + y[1], false, false);
+            n12 = (int32_t)(z[0] + z[1]);
         }
-        const int32_t duq = vg[0];
         const float sc = ch.sc;
         const int32_t dot = 2 * duq - 3 * sq;
         const int32_t c2 = c2_base - 8 * n12;
         const float t1 = (sc * sc) * 0.25f * (float)c2;
         const float t3 = (sc * qs) * (float)dot;
         const float dist = t1 - t3 + 0.0f;
-        const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)(ch.row0 + lane);
+        const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)(ch.base + lane);
         const uint64_t ts = __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const uint64_t tau = tau_w < ts ? tau_w : ts;
-        const bool take = lane < ch.nk && k64 < tau;
+        const bool take = lane >= ch.lo && lane < ch.hi && k64 < tau;
         const uint64_t mask = __ballot(take);
         if (take) {
             const int pos = wcount + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
@@ -457,78 +480,84 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             wl[pos] = k64;
         }
         wcount += __popcll(mask);
-        if (wcount > CAPW - 64 || (tau_w == NONE && wcount >= 256)) wave_compact();
+        if (wcount >= CAPW - 64) wave_compact();  // at most CAPW - 1 entries, sorted as CAPW
     };
 
-    // (Both halves run unconditionally: a chunk past the end has nk = 0 and
+    // Three chunks per wave in flight: while one is scored the next two load.
+    // (Every step runs unconditionally: a chunk past the end has lo == hi and
     // scores nothing, and the loop body stays free of branches around loads.)
     // The empty asm with a memory clobber pins each fetch's loads above the
     // scoring that follows (the compiler would otherwise sink them to their
     // first use); nothing reads the loaded registers there, so no wait is added.
-    Chunk ca, cb;
+    auto scan = [&](auto small) {
+        Chunk x0, x1, x2;
+        // Phase A: chunks wave and wave + 16 (2048 keys over the workgroup),
+        // every key kept; each wave sorts its 128 and publishes its E8-th
+        // smallest, and after one barrier every wave starts from the largest
+        // of those (about the 200th smallest of the 2048).
+        fetch(small, wave, x0);
+        fetch(small, wave + SW, x1);
+        fetch(small, wave + 2 * SW, x2);
+        asm volatile("" ::: "memory");
+        score(x0);
+        fetch(small, wave + 3 * SW, x0);
+        asm volatile("" ::: "memory");
+        score(x1);
+        fetch(small, wave + 4 * SW, x1);
+        asm volatile("" ::: "memory");
+        wave_compact();
+        __syncthreads();
+        refresh();
+        // Phase B: the rest, three chunks per trip.
+        for (int32_t g = wave + 2 * SW; g < nchunks; g += 3 * SW) {
+            score(x2);
+            fetch(small, g + 3 * SW, x2);
+            asm volatile("" ::: "memory");
+            score(x0);
+            fetch(small, g + 4 * SW, x0);
+            asm volatile("" ::: "memory");
+            score(x1);
+            fetch(small, g + 5 * SW, x1);
+            asm volatile("" ::: "memory");
+        }
+    };
     if (nchunks > 0) {  // uniform over the workgroup
-        // Phase A, in every wave: chunks wave and wave + 16 (2048 keys in all),
-        // every key kept.  One workgroup sort then gives the exact 128th
-        // smallest of them as the starting threshold of every wave; those 128
-        // stay in fin[0..128).
-        fetch(wave, ca);
-        fetch(wave + SW, cb);
-        asm volatile("" ::: "memory");
-        score(ca);
-        fetch(wave + 2 * SW, ca);
-        asm volatile("" ::: "memory");
-        score(cb);
-        __syncthreads();
-        for (int i = lane; i < wcount; i += 64) fin[atomicAdd(&count, 1)] = wl[i];
-        __syncthreads();
-        const int c0n = count;
-        const int n0 = pow2_at_least(c0n);
-        for (int i = c0n + tid; i < n0; i += STH) fin[i] = NONE;
-        __syncthreads();
-        bitonic_sort(fin, n0);
-        if (tid == 0) {
-            count = c0n < KMAX ? c0n : KMAX;
-            if (c0n >= KMAX) s_tau = fin[KMAX - 1];
-        }
-        wcount = 0;
-        __syncthreads();
-        // Phase B: the rest, two chunks per trip.
-        for (int32_t g = wave + 2 * SW; g < nchunks; g += 2 * SW) {
-            fetch(g + SW, cb);
-            asm volatile("" ::: "memory");
-            score(ca);
-            fetch(g + 2 * SW, ca);
-            asm volatile("" ::: "memory");
-            score(cb);
-        }
+        if (nrows < 64)
+            scan(std::integral_constant<bool, true>());
+        else
+            scan(std::integral_constant<bool, false>());
     }
-    // Final: every wave sorts its list and keeps its best 128; the keys at or
-    // below the shared threshold (with the starting set, a superset of the
-    // query's top 128) are gathered behind the starting set and sorted.
+    // Final: every wave sorts its list and keeps at most its best 128; the keys
+    // at or below the final threshold (a superset of the query's top 128, at
+    // most 16 x 128) are gathered, and each one's rank among them (keys are
+    // distinct: the index is part of the key) is its output position.
     wave_compact();
     __syncthreads();
-    const uint64_t tfin = s_tau;
-    for (int i = lane; i < wcount; i += 64) {
-        const uint64_t e = wl[i];
-        if (e <= tfin) fin[atomicAdd(&count, 1)] = e;
+    {
+        const uint64_t m = wave_max_u64(lane < SW ? s_e8[lane] : 0ull);
+        const uint64_t ts = s_tau;
+        const uint64_t tfin = m < ts ? m : ts;
+        for (int i = lane; i < wcount; i += 64) {
+            const uint64_t e = wl[i];
+            if (e <= tfin) fin[atomicAdd(&count, 1)] = e;
+        }
     }
     __syncthreads();
     const int cnt = count;
-    const int n = pow2_at_least(cnt);
-    for (int i = cnt + tid; i < n; i += STH) fin[i] = NONE;
-    __syncthreads();
-    bitonic_sort(fin, n);
     const float qn = s_qn;
-    for (int j = tid; j < k; j += STH) {
-        const uint64_t e = fin[j];
-        if (e == NONE) {
-            out_idx[q * k + j] = -1;
-            out_dist[q * k + j] = __builtin_inff();
-        } else {
+    for (int t = tid; t < cnt; t += STH) {
+        const uint64_t e = fin[t];
+        int r = 0;
+        for (int j = 0; j < cnt; j++) r += fin[j] < e;
+        if (r < k) {
             const float v = qn + unfkey((uint32_t)(e >> 32));
-            out_idx[q * k + j] = (int64_t)(uint32_t)e;
-            out_dist[q * k + j] = v > 0.f ? v : 0.f;
+            out_idx[q * k + r] = (int64_t)(uint32_t)e;
+            out_dist[q * k + r] = v > 0.f ? v : 0.f;
         }
+    }
+    for (int j = cnt + tid; j < k; j += STH) {
+        out_idx[q * k + j] = -1;
+        out_dist[q * k + j] = __builtin_inff();
     }
 }
 

@@ -74,6 +74,21 @@ def test_search_small_with_edge_cases(dev):
     assert sorted(idx[2][:3]) == [0 + sizes[0], 1 + sizes[0], 2 + sizes[0]] and np.all(idx[2][3:] == -1)
 
 
+@pytest.mark.parametrize("sizes", [[1], [0, 37], [20, 0, 43], [64], [30, 35], [1, 128, 1], [64, 64, 2]])
+def test_search_stores_near_one_chunk(dev, sizes):
+    # Stores of fewer than 64 keys are read key by key; from 64 keys on, a
+    # chunk is read as the 64 keys that end at the store's last row when it
+    # would run past it.  Both sides of that boundary, every cell probed.
+    rng = np.random.default_rng(len(sizes) * 100 + sum(sizes))
+    sizes = np.array(sizes)
+    store, codes, scales, cs = make_store(dev, sizes, 13)
+    nq, ncells = 5, len(sizes)
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.permutation(ncells) for _ in range(nq)]).astype(np.int32)
+    for k in (128, 3):
+        check_search(dev, store, codes, scales, cs, queries, probes, k)
+
+
 def test_search_ties_break_by_key_index(dev):
     # Identical keys give identical scores: the kept ones must be the lowest indices.
     base = np.random.default_rng(4).standard_normal(D).astype(np.float32)
