@@ -197,7 +197,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     __shared__ uint64_t s_e8[SW];         // each wave's E8-th smallest kept key
     __shared__ int16_t s_Q[D];
     __shared__ float s_qs, s_qn;
-    __shared__ int32_t s_sq, s_np, count;
+    __shared__ int32_t s_sq, s_np, count, s_next;
     __shared__ int32_t s_cell[PROBE_MAX], s_share[PROBE_MAX];
     __shared__ int64_t s_c0[PROBE_MAX], s_c1[PROBE_MAX];
     __shared__ int64_t s_r0[PROBE_MAX], s_nrows;
@@ -254,6 +254,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         if (lane == 0) {
             s_tau = NONE;
             count = 0;
+            s_next = 0;
         }
     }
     __syncthreads();
@@ -350,9 +351,11 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     const int64_t nrows = s_nrows;
     const int32_t c2_base = 9 * D;
 
-    // Wave w scans chunks w, w + 16, ... of the query's cells taken in order (a
-    // chunk is the up to 64 keys of one cell at rows row0 .. row0 + nk; the
-    // chunk -> (cell, row) map is uniform per wave).  A chunk is read as the 64
+    // The waves take chunks of the query's cells (taken in order) from a
+    // shared counter, so each wave's chunks come in increasing order and a fast
+    // wave simply scans more of them (a chunk is the up to 64 keys of one cell
+    // at rows row0 .. row0 + nk; the chunk -> (cell, row) map is uniform per
+    // wave).  A chunk is read as the 64
     // keys from base = min(row0, nrows - 64), so the loads of a chunk are four
     // fixed offsets from one address and never leave the store; lane l scores
     // key base + l and keeps it when lo <= l < hi.  For group G (keys 16G ..
@@ -366,13 +369,17 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         uint4 c[4];
         float sc;
         int64_t base;
-        int32_t lo, hi;
+        int32_t lo, hi, g;
     };
     int32_t c0 = 0;
     while (c0 < np - 1 && s_cpre[c0 + 1] == 0) c0++;
     const int64_t safe_row0 = nchunks > 0 ? s_r0[c0] : 0;
-    auto fetch = [&](auto small, int32_t g, Chunk &ch) {
+    auto fetch = [&](auto small, Chunk &ch) {
         constexpr bool SMALL = decltype(small)::value;
+        int32_t gl = 0;
+        if (lane == 0) gl = atomicAdd(&s_next, 1);
+        const int32_t g = __builtin_amdgcn_readfirstlane(gl);
+        ch.g = g;
         while (ccell < np - 1 && g >= s_cpre[ccell + 1]) ccell++;
         const bool live = g < nchunks;
         const int32_t key0 = (g - s_cpre[ccell]) * 64;
@@ -491,33 +498,35 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     // first use); nothing reads the loaded registers there, so no wait is added.
     auto scan = [&](auto small) {
         Chunk x0, x1, x2;
-        // Phase A: chunks wave and wave + 16 (2048 keys over the workgroup),
-        // every key kept; each wave sorts its 128 and publishes its E8-th
+        // Phase A: each wave's first two chunks (2048 keys over the
+        // workgroup), every key kept; each wave sorts its 128 and publishes its E8-th
         // smallest, and after one barrier every wave starts from the largest
         // of those (about the 200th smallest of the 2048).
-        fetch(small, wave, x0);
-        fetch(small, wave + SW, x1);
-        fetch(small, wave + 2 * SW, x2);
+        fetch(small, x0);
+        fetch(small, x1);
+        fetch(small, x2);
         asm volatile("" ::: "memory");
         score(x0);
-        fetch(small, wave + 3 * SW, x0);
+        fetch(small, x0);
         asm volatile("" ::: "memory");
         score(x1);
-        fetch(small, wave + 4 * SW, x1);
+        fetch(small, x1);
         asm volatile("" ::: "memory");
         wave_compact();
         __syncthreads();
         refresh();
-        // Phase B: the rest, three chunks per trip.
-        for (int32_t g = wave + 2 * SW; g < nchunks; g += 3 * SW) {
+        // Phase B: the rest, three chunks per trip (x2, x0, x1 hold this
+        // wave's next chunks in increasing order: once x2's is past the end,
+        // so are the others).
+        while (x2.g < nchunks) {
             score(x2);
-            fetch(small, g + 3 * SW, x2);
+            fetch(small, x2);
             asm volatile("" ::: "memory");
             score(x0);
-            fetch(small, g + 4 * SW, x0);
+            fetch(small, x0);
             asm volatile("" ::: "memory");
             score(x1);
-            fetch(small, g + 5 * SW, x1);
+            fetch(small, x1);
             asm volatile("" ::: "memory");
         }
     };
