@@ -14,6 +14,8 @@ reference CPU path, one thread) on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import hashlib
 import json
 import os
 import platform
@@ -33,6 +35,58 @@ LAYERS = [("qkv", 256, 768), ("out", 256, 256), ("ffn1", 256, 1024), ("ffn2", 10
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+@contextlib.contextmanager
+def one_core():
+    """Pins this process to one host core for a single-thread CPU baseline."""
+    try:
+        old = os.sched_getaffinity(0)
+        core = min(old)
+        os.sched_setaffinity(0, {core})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        yield
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+
+
+def source_hash(rel):
+    """sha256 of a kernel source file: ties a committed rocprof counter summary to the code it measured."""
+    with open(os.path.join(ROOT, rel), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def traffic_for(kernel_key, src_rel):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) from profiles/traffic.json, or None when that
+    summary was taken on a different version of the kernel's source."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = t.get(kernel_key)
+    if not e or e.get("source_sha256_16") != source_hash(src_rel):
+        return None
+    return int(e["fetch_bytes"] + e["write_bytes"])
+
+
+def roofline(kernel, flops, nbytes, ms, traffic=None):
+    """Roofline entry for one kernel: the binding roof is the lower of MFMA peak and intensity x HBM peak."""
+    tflops = flops / ms / 1e9
+    gbs = nbytes / ms / 1e6
+    ridge = PEAK["f16"] * 1e12 / (PEAK["hbm_gbs"] * 1e9)
+    if flops / nbytes < ridge:
+        r = dict(kernel=kernel, bound="hbm", achieved=round(gbs, 1), peak=PEAK["hbm_gbs"], unit="GB/s",
+                 frac=round(gbs / PEAK["hbm_gbs"], 4))
+    else:
+        r = dict(kernel=kernel, bound="mfma", achieved=round(tflops, 2), peak=PEAK["f16"], unit="TFLOP/s",
+                 frac=round(tflops / PEAK["f16"], 4))
+    r.update(traffic=traffic, algorithmic_bytes=int(nbytes), flops=int(flops), ms=round(ms, 5),
+             tflops=round(tflops, 2), mfma_frac=round(tflops / PEAK["f16"], 4), hbm_gbs=round(gbs, 1))
+    return r
 
 
 def cpu_model():
@@ -153,21 +207,31 @@ def check_gemm_set(ss, use_f16, which=(2, 5, 8)):
     return max(errs)
 
 
-def cpu_gemm_baseline(ss):
-    """The reference CPU path (NdArray::matmul, with the explicit transposes the tape makes) on one full step set."""
+def cpu_gemm_baseline(ss, budget_s=10.0):
+    """The reference CPU path (NdArray::matmul, with the explicit transposes the tape makes) on full step sets:
+    repeated for about `budget_s` seconds (at least 5 sets), one pinned core, median set time reported."""
     import oracle
     host = [(a["h"].cpu().numpy(), b["h"].cpu().numpy(), a.get("trans", False), b.get("trans", False), m, k, n)
             for _, a, b, _, m, k, n in ss.calls]
-    t0 = time.perf_counter()
-    for A, B, ta, tb, m, k, n in host:
-        A2 = oracle.transpose(A.reshape(k, m)) if ta else A.reshape(m, k)
-        B2 = oracle.transpose(B.reshape(n, k)) if tb else B.reshape(k, n)
-        oracle.matmul(A2, B2)
-    dt = time.perf_counter() - t0
+
+    def one_set():
+        t0 = time.perf_counter()
+        for A, B, ta, tb, m, k, n in host:
+            A2 = oracle.transpose(A.reshape(k, m)) if ta else A.reshape(m, k)
+            B2 = oracle.transpose(B.reshape(n, k)) if tb else B.reshape(k, n)
+            oracle.matmul(A2, B2)
+        return time.perf_counter() - t0
+
+    with one_core():
+        times = [one_set()]
+        while len(times) < 5 or sum(times) < budget_s:
+            times.append(one_set())
+    dt = float(np.median(times))
     return dict(value=round(ss.flops / dt / 1e12, 5), unit="TFLOP/s", cores=1, kind="port",
-                sample="one full d=256 step GEMM set (15 GEMMs, 20.9 GFLOP) through the oracle's restatement of "
-                       "NdArray::matmul (tensor.rs:248-276) incl. the tape's explicit transposes, 1 thread, "
-                       f"gcc -O3 -mavx2 -mfma -ffp-contract=off, {cpu_model()}", seconds=round(dt, 3))
+                sample=f"{len(times)} full d=256 step GEMM sets (15 GEMMs, 20.9 GFLOP each; median set time) "
+                       "through the oracle's restatement of NdArray::matmul (tensor.rs:248-276) incl. the tape's "
+                       "explicit transposes, 1 pinned thread, gcc -O3 -mavx2 -mfma -ffp-contract=off, "
+                       f"{cpu_model()}", seconds=round(sum(times), 3))
 
 
 # --------------------------------------------------------------------------- smaller GEMM configs
@@ -222,21 +286,28 @@ def bench_attention(dev, stream, steps, warmup, use_f16):
                 tflops=round(flops / graph_ms / 1e9, 3))
 
 
-def cpu_attention_baseline():
+def cpu_attention_baseline(reps=20):
     import oracle
     b, h, t, hd = 32, 4, 128, 64
     rng = oracle.Rng(3)
     q, k, v, do = (rng.gaussian(b * h * t * hd) for _ in range(4))
-    t0 = time.perf_counter()
-    oracle.attention_fwd_bwd(q, k, v, do, b * h, t, hd, hd ** -0.5)
-    dt = time.perf_counter() - t0
+    times = []
+    with one_core():
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            oracle.attention_fwd_bwd(q, k, v, do, b * h, t, hd, hd ** -0.5)
+            times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
     flops = 6 * b * h * 2 * t * t * hd
-    return dict(value=round(flops / dt / 1e12, 5), unit="TFLOP/s", cores=1, kind="port", seconds=round(dt, 3),
-                sample="one full attention fwd+bwd (128 chunks of 128x128x64) through the per-chunk loop of "
-                       "tape.rs:73-112 restated in the oracle, 1 thread")
+    return dict(value=round(flops / dt / 1e12, 5), unit="TFLOP/s", cores=1, kind="port", seconds=round(sum(times), 3),
+                sample=f"{reps} full attention fwd+bwd passes (128 chunks of 128x128x64 each; median) through the "
+                       "per-chunk loop of tape.rs:73-112 restated in the oracle, 1 pinned thread")
 
 
 # --------------------------------------------------------------------------- kNN
+
+NQ_CPU = 256  # queries of one batch scored by the CPU baseline (a whole batch, about 4 s of one core)
+
 
 class KnnBench:
     N, NCELLS, NQ, NPROBE, D = 125_000_000, 12288, 256, 8, 256
@@ -306,8 +377,8 @@ class KnnBench:
                 return False
         return True
 
-    def cpu_baseline(self, nq=24):
-        """The oracle's exact 2-bit scoring + top-128 over the same probed cells, 1 thread."""
+    def cpu_baseline(self, nq=NQ_CPU):
+        """The oracle's exact 2-bit scoring + top-128 over the same probed cells, 1 pinned thread."""
         import torch
         import oracle
         bt = self.batches[1]
@@ -318,15 +389,17 @@ class KnnBench:
             sub = np.concatenate([[0], np.cumsum([self.cs[c + 1] - self.cs[c] for c in cells])]).astype(np.int64)
             sel = torch.from_numpy(rows).to(self.codes.device)
             codes, scales = self.codes[sel].cpu().numpy(), self.scales[sel].cpu().numpy()
-            t0 = time.perf_counter()
-            oracle.knn_search(codes, scales, sub, bt["qh"][qi:qi + 1], np.arange(len(cells), dtype=np.int32)[None], 128)
-            dt += time.perf_counter() - t0
+            with one_core():
+                t0 = time.perf_counter()
+                oracle.knn_search(codes, scales, sub, bt["qh"][qi:qi + 1],
+                                  np.arange(len(cells), dtype=np.int32)[None], 128)
+                dt += time.perf_counter() - t0
             total_pairs += rows.size
         return dict(value=round(total_pairs / dt / 1e9, 5), unit="G keys/s", cores=1, kind="port",
                     seconds=round(dt, 3),
                     sample=f"{nq} queries x 8 probed cells of the 125M-key store ({total_pairs} pairs), exact 2-bit "
-                           "scoring + top-128 by (score, index) in the oracle (C, 1 thread); the reference has no "
-                           "CPU quantised scorer")
+                           "scoring + top-128 by (score, index) in the oracle (C, 1 pinned thread); the reference has "
+                           "no CPU quantised scorer")
 
 
 # --------------------------------------------------------------------------- main
@@ -379,10 +452,10 @@ def main():
             sys.exit(3)
         dom = max(calls16, key=lambda c: c["ms"])
         value = ss16.flops / graph16 / 1e9
-        roof = dict(kernel=f"k_gemm f16 ({dom['gemm']}: {dom['m']}x{dom['k']}x{dom['n']})", bound="mfma",
-                    achieved=dom["tflops"], peak=PEAK["f16"], unit="TFLOP/s",
-                    frac=round(dom["tflops"] / PEAK["f16"], 4), traffic=None,
-                    hbm_gbs=dom["gbs"], hbm_frac=round(dom["gbs"] / PEAK["hbm_gbs"], 4))
+        dm, dk, dn = dom["m"], dom["k"], dom["n"]
+        roof = roofline(f"k_gemm f16 ({dom['gemm']}: {dm}x{dk}x{dn})", 2 * dm * dk * dn,
+                        4 * (dm * dk + dk * dn + dm * dn), dom["ms"],
+                        traffic_for(f"k_gemm f16 {dom['gemm']}", "scratchtape_amd/csrc/gemm.hip"))
         extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes, graph_ms=round(graph16, 5),
                                    eager_ms=round(eager16, 5), tflops=round(value, 2),
                                    mfma_frac=round(value / PEAK["f16"], 4),
@@ -429,7 +502,9 @@ def main():
                    distinct_cell_bytes=int(byts), hbm_gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK["hbm_gbs"], 4),
                    roofline=dict(kernel="k_search (st_knn_search_ivf_2bit: one fused launch)", bound="hbm",
                                  achieved=round(gbs, 1), peak=PEAK["hbm_gbs"], unit="GB/s",
-                                 frac=round(gbs / PEAK["hbm_gbs"], 4), traffic=None),
+                                 frac=round(gbs / PEAK["hbm_gbs"], 4),
+                                 traffic=traffic_for("k_search", "scratchtape_amd/csrc/knn.hip"),
+                                 algorithmic_bytes=int(byts)),
                    store_gen_s=round(kb.gen_s, 3))
         if not args.no_cpu:
             knn["cpu_baseline"] = kb.cpu_baseline()
