@@ -7,13 +7,13 @@
  *  - Device buffers are plain device pointers (the reference's cubecl
  *    `Handle`s).  The caller owns every operand and output; outputs are
  *    written in place.  The library owns only a grow-only scratch arena per
- *    device (split-k partials, kNN candidate lists), like the reference's
- *    `split_scratch` (gpu_step/matmul.rs:207-217) and `KnnStore::scratch`
- *    (gpu_step/knn.rs:74-105).
+ *    device (split-k partials), like the reference's `split_scratch`
+ *    (gpu_step/matmul.rs:207-217); the kNN search keeps its candidate lists
+ *    in LDS and allocates nothing.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL is the default
  *    stream) and is asynchronous, as the reference's single in-order queue
  *    (gpu_step/mod.rs:42, 78).  Calls that use the scratch arena (split-k
- *    GEMMs, kNN search) must be serialised on one stream per device.
+ *    GEMMs) must be serialised on one stream per device.
  *  - The reference panics (assert!/expect) on bad arguments.  Panics cannot
  *    cross an FFI boundary, so every entry point returns an st_status and
  *    st_last_error() gives the message (thread-local), whose text follows
@@ -138,7 +138,9 @@ st_status st_knn_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t 
  * query, the k (<= 128, KMAX knn.rs:21) nearest by the exact 2-bit score,
  * ascending by (distance, key index): out_idx [nq, k] global rows (-1
  * padding), out_dist [nq, k] = max(|q^|^2 + dist, 0) (+inf padding).
- * All pointers are device pointers; d == 256. */
+ * All pointers are device pointers; d == 256; the store holds fewer than
+ * 2^32 keys (cell_start[ncells] < 2^32: key indices are 32-bit inside the
+ * top-k keys). */
 st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *scales,
                                  const int64_t *cell_start, int64_t ncells, int64_t max_cell,
                                  const float *queries, const int32_t *probes, int64_t nq,
