@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gemm_dma.h"
 
 namespace {
 
@@ -445,6 +446,45 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
     const int64_t lda = a->ld ? a->ld : (a->trans ? m : k);
     const int64_t ldb = b->ld ? b->ld : (b->trans ? k : n);
     const int64_t ldo = out->ld ? out->ld : n;
+
+    // Tile-divisible, 16-byte aligned problems run on the LDS-DMA kernel.
+    {
+        st::DmaGemm d;
+        std::memset(&d, 0, sizeof d);
+        d.a = a->p + a->off;
+        d.a_stride = a->stride;
+        d.a_group = ag;
+        d.a_inner = a->inner;
+        d.lda = lda;
+        d.ta = a->trans != 0;
+        d.b = b->p + b->off;
+        d.b_stride = b->stride;
+        d.b_group = bg;
+        d.b_inner = b->inner;
+        d.ldb = ldb;
+        d.tb = b->trans != 0;
+        d.out = out->p + out->off;
+        d.o_stride = out->stride;
+        d.o_group = og;
+        d.o_inner = out->inner;
+        d.ldo = ldo;
+        d.bias = epi.bias ? epi.bias + epi.bias_off : nullptr;
+        d.bias_stride = epi.bias_stride;
+        d.mask = epi.mask ? epi.mask + epi.mask_off : nullptr;
+        d.res = epi.residual ? epi.residual + epi.residual_off : nullptr;
+        d.cs = out->p + epi.col_sum_off;
+        d.cs_stride = epi.col_sum_stride;
+        d.has_cs = epi.has_col_sum;
+        d.relu = epi.relu;
+        d.accumulate = epi.accumulate;
+        d.f16 = f16;
+        d.batch = batch;
+        d.m = m;
+        d.k = k;
+        d.n = n;
+        st_status ds = ST_OK;
+        if (st::gemm_dma(d, stream, &ds)) return ds;
+    }
 
     TileCfg tc = choose_tile(batch, m, n);
     const int BK = f16 ? 64 : 32;

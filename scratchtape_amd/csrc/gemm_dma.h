@@ -1,0 +1,38 @@
+// Internal interface between the GEMM entry points (gemm.hip) and the
+// LDS-DMA GEMM (gemm_dma.hip).
+#pragma once
+
+#include "common.h"
+
+namespace st {
+
+// One batched GEMM out[z] (+)= epi(a[z] @ b[z]); operand pointers already
+// include their element offsets; z addresses a matrix as
+// (z / group) * stride + (z % group) * inner.
+struct DmaGemm {
+    const float *a;
+    int64_t a_stride, a_group, a_inner, lda;
+    int32_t ta;
+    const float *b;
+    int64_t b_stride, b_group, b_inner, ldb;
+    int32_t tb;
+    float *out;
+    int64_t o_stride, o_group, o_inner, ldo;
+    const float *bias;  // + bias_off
+    int64_t bias_stride;
+    const float *mask;  // + mask_off
+    const float *res;   // + residual_off
+    float *cs;          // out buffer + col_sum_off
+    int64_t cs_stride;
+    int32_t has_cs, relu, accumulate;
+    int32_t f16;
+    int64_t batch, m, k, n;
+};
+
+// Enqueues the GEMM on the LDS-DMA kernel when the shape and alignment allow
+// it (tile-divisible m and n, k % 32 == 0, 16-byte aligned operands and
+// strides).  Returns false, having enqueued nothing, when they do not;
+// otherwise true, with *status the launch status.
+bool gemm_dma(const DmaGemm &g, hipStream_t stream, st_status *status);
+
+}  // namespace st

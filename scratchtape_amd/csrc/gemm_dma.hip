@@ -1,0 +1,500 @@
+// GEMM on gfx950 with operand tiles moved global -> LDS by the DMA path of
+// global_load_lds_dwordx4: no register staging, NS - 1 k-stages in flight, one
+// barrier per stage.  f16-in/f32-accumulate (v_mfma_f32_16x16x32_f16, f32
+// rounded to f16 to nearest even when a fragment is read from LDS) and f32
+// (v_mfma_f32_16x16x4_f32).  Semantics: gpu_step/matmul.rs:26-299 (MatRef
+// addressing, the epilogue in the reference's order, deterministic split-k).
+//
+// LDS layouts (f32, one 32-deep k-stage per operand; a DMA wave-load writes
+// 64 x 16-byte chunks to consecutive LDS slots, so the layout is chosen on the
+// global-address side):
+//  - KC, an operand whose k is contiguous in memory (A not transposed, B
+//    transposed): [row][8 chunks of 4 k]; chunk c of row r sits in slot
+//    r * 8 + (c ^ ((r >> 1) & 7)).  A fragment (8 k of one row per lane) is two
+//    128-bit reads; the swizzle puts the 16 rows a quarter-wave reads in 16
+//    distinct 16-byte bank groups.
+//  - RC, an operand whose rows are contiguous (A transposed, B not): [k][rows],
+//    line kk holding rows in chunks of 4 rotated by 16 rows per group of 8 k:
+//    chunk q of line kk sits in slot kk * Q + (q + 4 * ((kk >> 3) & 3)) % Q,
+//    Q = ROWS / 4.  A fragment is eight 32-bit reads; the 64 lanes of each read
+//    hit 64 distinct banks.
+//
+// The finished tile goes through LDS once more so that every store (and every
+// epilogue load) moves whole 16-byte runs of a row.  Split-k (few output
+// tiles, free epilogue): each slice writes its partial tile to the scratch
+// arena and k_sum_slices adds the slices in ascending order (deterministic),
+// with accumulate and the column sums, as the reference's k_split_sum
+// (matmul.rs:259-299).
+#include <algorithm>
+#include <cstring>
+#include <type_traits>
+
+#include "gemm_dma.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int THREADS = 256;
+constexpr int BK = 32;  // k per stage
+
+struct KArgs {
+    const float *a, *b;
+    int64_t a_stride, a_group, a_inner, lda;
+    int64_t b_stride, b_group, b_inner, ldb;
+    float *out;  // the output, or the split partials [batch][splits][m][n]
+    int64_t o_stride, o_group, o_inner, ldo;
+    const float *bias;
+    int64_t bias_stride;
+    const float *mask, *res;
+    float *cs;  // column-sum destination (out buffer + col_sum_off), or the split partials
+    int64_t cs_stride;
+    int32_t has_cs, relu, accumulate;
+    int32_t m, n, k, splits, slice_k;
+};
+
+// 16 bytes per lane from global memory to LDS: lane l's 16 bytes from gptr
+// land at LDS byte address lds_addr + 16 l (lds_addr wave-uniform, passed in
+// M0).  Issued as inline assembly so that the compiler sees no LDS store in
+// flight: it would otherwise wait for every DMA before each LDS read (it cannot
+// tell which stage a DMA writes).  Completion is tracked by this file's
+// explicit vmcnt waits, followed by a workgroup barrier, before any wave reads
+// the stage.  M0 is saved and restored around the load, so the compiler's view
+// of it stays valid, and one wait state separates the M0 write from the LDS
+// DMA that reads it (a gfx9 hazard the compiler does not guard in inline asm).
+__device__ __forceinline__ void dma16(const float *gptr, uint32_t lds_addr) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(gptr), "s"(lds_addr)
+        : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr_of(const float *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+}
+
+// Waits until at most N vector-memory instructions of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Waits until this wave's DMA of the oldest stage in flight has landed, with
+// `ahead` (0 .. MAXA) younger stages of L instructions each still in flight.
+template <int L, int MAXA>
+__device__ __forceinline__ void wait_stage(int ahead) {
+    if constexpr (MAXA >= 4) {
+        if (ahead >= 4) return wait_vm<4 * L>();
+    }
+    if constexpr (MAXA >= 3) {
+        if (ahead == 3) return wait_vm<3 * L>();
+    }
+    if constexpr (MAXA >= 2) {
+        if (ahead == 2) return wait_vm<2 * L>();
+    }
+    if constexpr (MAXA >= 1) {
+        if (ahead == 1) return wait_vm<L>();
+    }
+    wait_vm<0>();
+}
+
+// Workgroup barrier without the memory fence of __syncthreads() (which would
+// wait for every load of this wave, the DMA of the younger stages included);
+// the empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void bar() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Element offset (from the operand's matrix base, at k = 0) of the 16 bytes
+// that DMA slot p of a ROWS x 32 stage tile receives.
+template <int ROWS, bool KC>
+__device__ __forceinline__ int64_t slot_src(int p, int64_t ld, int row0) {
+    if constexpr (KC) {
+        const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
+        return (int64_t)(row0 + r) * ld + 4 * c;
+    } else {
+        constexpr int Q = ROWS / 4;
+        const int kk = p / Q, s = p % Q;
+        const int q = (s - 4 * ((kk >> 3) & 3) + 4 * Q) % Q;
+        return (int64_t)kk * ld + row0 + 4 * q;
+    }
+}
+
+// The 8 values (k = 8g .. 8g + 7 of the stage) of row r of a stage tile.
+template <int ROWS, bool KC>
+__device__ __forceinline__ void frag(const float *t, int r, int g, float (&x)[8]) {
+    if constexpr (KC) {
+        const int sw = (r >> 1) & 7;
+        const f32x4 lo = *reinterpret_cast<const f32x4 *>(t + (r * 8 + ((2 * g) ^ sw)) * 4);
+        const f32x4 hi = *reinterpret_cast<const f32x4 *>(t + (r * 8 + ((2 * g + 1) ^ sw)) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = lo[e];
+            x[4 + e] = hi[e];
+        }
+    } else {
+        constexpr int Q = ROWS / 4;
+        const int q = ((r >> 2) + 4 * g) % Q;  // (kk >> 3) & 3 == g for kk = 8g + u
+#pragma unroll
+        for (int u = 0; u < 8; u++) x[u] = t[((8 * g + u) * Q + q) * 4 + (r & 3)];
+    }
+}
+
+__device__ __forceinline__ int64_t zoff(int64_t z, int64_t group, int64_t stride, int64_t inner) {
+    return (z / group) * stride + (z % group) * inner;
+}
+
+// NS k-stages resident in LDS, NS - 1 of them in flight while one is multiplied.
+template <int BM, int BN, int NS, bool TA, bool TB, bool F16>
+__global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
+    constexpr bool AKC = !TA, BKC = TB;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int LA = BM / 32, LB = BN / 32;  // DMA wave-loads per wave per stage
+    constexpr int SA = BM * BK, SB = BN * BK;  // floats per stage
+    constexpr int TP = BN + 4;                 // row pitch of the staged output tile
+    static_assert(BM * TP <= NS * (SA + SB), "output tile fits the stage ring");
+    __shared__ __attribute__((aligned(16))) float lds[NS * (SA + SB)];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // Workgroups go to the 8 XCDs round-robin by linear id: remap so each XCD
+    // gets a contiguous run of tiles (sharing operand panels in its L2).
+    int64_t lin = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+    const int64_t total = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+    const int bx = (int)(lin % gridDim.x);
+    const int by = (int)((lin / gridDim.x) % gridDim.y);
+    const int64_t z = lin / ((int64_t)gridDim.x * gridDim.y);
+    const int64_t zb = z / g.splits;
+    const int slice = (int)(z % g.splits);
+    const int row0 = by * BM, col0 = bx * BN;
+    const int kbeg = slice * g.slice_k;
+    const int kend = min(g.k, kbeg + g.slice_k);
+    const int nst = (kend - kbeg) / BK;
+    const bool do_cs = g.has_cs && by == 0;
+
+    const float *abase = g.a + zoff(zb, g.a_group, g.a_stride, g.a_inner);
+    const float *bbase = g.b + zoff(zb, g.b_group, g.b_stride, g.b_inner);
+    int64_t aoff[LA], boff[LB];
+#pragma unroll
+    for (int j = 0; j < LA; j++)
+        aoff[j] = slot_src<BM, AKC>((wave * LA + j) * 64 + lane, g.lda, row0) + (AKC ? kbeg : (int64_t)kbeg * g.lda);
+#pragma unroll
+    for (int j = 0; j < LB; j++)
+        boff[j] = slot_src<BN, BKC>((wave * LB + j) * 64 + lane, g.ldb, col0) + (BKC ? kbeg : (int64_t)kbeg * g.ldb);
+    const int64_t astep = AKC ? BK : (int64_t)BK * g.lda, bstep = BKC ? BK : (int64_t)BK * g.ldb;
+
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    auto issue = [&](int st) {
+        const uint32_t base = lds_addr_of(lds + (st % NS) * (SA + SB));
+#pragma unroll
+        for (int j = 0; j < LA; j++) dma16(abase + aoff[j] + st * astep, base + (wave_u * LA + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < LB; j++) dma16(bbase + boff[j] + st * bstep, base + SA * 4 + (wave_u * LB + j) * 1024);
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < BN), this slice
+
+    // Stage st lives in ring slot st % NS.  Per stage: wait for this wave's DMA
+    // of stage st (younger stages stay in flight), barrier (every wave's part
+    // of stage st has landed, and every wave is done reading stage st - 1),
+    // start stage st + NS - 1 into stage st - 1's slot, multiply stage st.
+    auto step = [&](int st) {
+        wait_stage<LA + LB, NS - 2>(min(NS - 2, nst - 1 - st));
+        bar();
+        if (st + NS - 1 < nst) issue(st + NS - 1);
+        const float *la = lds + (st % NS) * (SA + SB);
+        const float *lb = la + SA;
+        const int gq = lane >> 4;
+        if constexpr (F16) {
+            half8 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                float x[8];
+                frag<BM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, x);
+#pragma unroll
+                for (int e = 0; e < 8; e++) af[i][e] = (_Float16)x[e];
+            }
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                float x[8];
+                frag<BN, BKC>(lb, wn * WN + j * 16 + (lane & 15), gq, x);
+#pragma unroll
+                for (int e = 0; e < 8; e++) bf[j][e] = (_Float16)x[e];
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        } else {
+            // Lane group gq supplies k = 8 gq + u at MFMA step u, for A and B alike.
+            float ax[FM][8], bx8[FN][8];
+#pragma unroll
+            for (int i = 0; i < FM; i++) frag<BM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, ax[i]);
+#pragma unroll
+            for (int j = 0; j < FN; j++) frag<BN, BKC>(lb, wn * WN + j * 16 + (lane & 15), gq, bx8[j]);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[i][u], bx8[j][u], acc[i][j], 0, 0, 0);
+        }
+        if (do_cs && tid < BN) {
+            // This stage's 32 values of column col0 + tid, added in k order.
+            float x[8];
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) {
+                frag<BN, BKC>(lb, tid, gg, x);
+#pragma unroll
+                for (int e = 0; e < 8; e++) cs_acc += x[e];
+            }
+        }
+    };
+
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+        if (st < nst) issue(st);
+    for (int st = 0; st < nst; st++) step(st);
+
+    if (do_cs && tid < BN) {
+        if (g.splits > 1)
+            g.cs[(zb * g.splits + slice) * (int64_t)g.n + col0 + tid] = cs_acc;
+        else
+            g.cs[zb * g.cs_stride + col0 + tid] += cs_acc;
+    }
+
+    // Output tile -> LDS (row pitch TP: the 16 lanes of a row write 16
+    // consecutive words and the 4 row groups land 16 banks apart) -> whole
+    // 16-byte runs of rows to memory, with the epilogue in the reference's
+    // order: + bias, ReLU, zero where mask <= 0, + residual, + out.
+    bar();  // every wave is done with the stage ring
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                lds[(wm * WM + i * 16 + 4 * (lane >> 4) + r) * TP + wn * WN + j * 16 + (lane & 15)] = acc[i][j][r];
+    bar();
+    if (g.splits > 1) {
+        float *P = g.out + (zb * g.splits + slice) * (int64_t)g.m * g.n;
+        for (int e = tid; e < BM * BN / 4; e += THREADS) {
+            const int r = e / (BN / 4), c4 = (e % (BN / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(P + (int64_t)(row0 + r) * g.n + col0 + c4) =
+                *reinterpret_cast<const f32x4 *>(lds + r * TP + c4);
+        }
+        return;
+    }
+    const int64_t o0 = zoff(zb, g.o_group, g.o_stride, g.o_inner);
+    for (int e = tid; e < BM * BN / 4; e += THREADS) {
+        const int r = e / (BN / 4), c4 = (e % (BN / 4)) * 4;
+        f32x4 v = *reinterpret_cast<const f32x4 *>(lds + r * TP + c4);
+        const int col = col0 + c4;
+        const int64_t idx = o0 + (int64_t)(row0 + r) * g.ldo + col;
+        if (g.bias) {
+            const float *bp = g.bias + zb * g.bias_stride + col;
+#pragma unroll
+            for (int x = 0; x < 4; x++) v[x] += bp[x];
+        }
+        if (g.relu) {
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                if (v[x] < 0.f) v[x] = 0.f;
+        }
+        if (g.mask) {
+            const f32x4 mk = *reinterpret_cast<const f32x4 *>(g.mask + idx);
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                if (mk[x] <= 0.f) v[x] = 0.f;
+        }
+        if (g.res) v += *reinterpret_cast<const f32x4 *>(g.res + idx);
+        if (g.accumulate) v += *reinterpret_cast<const f32x4 *>(g.out + idx);
+        *reinterpret_cast<f32x4 *>(g.out + idx) = v;
+    }
+}
+
+// out[b] (+)= sum over s (ascending) of partial[b][s], 4 elements per thread;
+// then the column-sum partials into their destination (always +=).
+__global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ part, float *out, int64_t mn,
+                                                    int32_t splits, int64_t o_stride, int64_t batch,
+                                                    int32_t accumulate, const float *cs_part, float *cs_dst,
+                                                    int64_t cs_stride, int64_t n) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t q = mn / 4;
+    if (e < batch * q) {
+        const int64_t b = e / q, i = e % q;
+        const f32x4 *p = reinterpret_cast<const f32x4 *>(part) + b * splits * q + i;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < splits; s++) v += p[s * q];
+        f32x4 *o = reinterpret_cast<f32x4 *>(out + b * o_stride) + i;
+        if (accumulate) v += *o;
+        *o = v;
+    } else if (cs_part) {
+        const int64_t c = e - batch * q;
+        if (c < batch * n) {
+            const int64_t b = c / n, j = c % n;
+            float v = 0.f;
+            for (int s = 0; s < splits; s++) v += cs_part[(b * splits + s) * n + j];
+            cs_dst[b * cs_stride + j] += v;
+        }
+    }
+}
+
+using KernelFn = void (*)(KArgs);
+
+template <int BM, int BN, int NS, bool F16>
+KernelFn pick(bool ta, bool tb) {
+    if (!ta && !tb) return &k_gemm_dma<BM, BN, NS, false, false, F16>;
+    if (!ta && tb) return &k_gemm_dma<BM, BN, NS, false, true, F16>;
+    if (ta && !tb) return &k_gemm_dma<BM, BN, NS, true, false, F16>;
+    return &k_gemm_dma<BM, BN, NS, true, true, F16>;
+}
+
+template <int BM, int BN, int NS>
+KernelFn pick2(bool f16, bool ta, bool tb) {
+    return f16 ? pick<BM, BN, NS, true>(ta, tb) : pick<BM, BN, NS, false>(ta, tb);
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+namespace st {
+
+bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
+    const int64_t m = d.m, n = d.n, k = d.k, batch = d.batch;
+    if (k <= 0 || k % BK != 0) return false;
+    // 16-byte runs everywhere: operands for the DMA, out / mask / residual for
+    // the vector epilogue.
+    if (!al16(d.a) || !al16(d.b) || d.lda % 4 || d.ldb % 4 || d.a_stride % 4 || d.a_inner % 4 || d.b_stride % 4 ||
+        d.b_inner % 4)
+        return false;
+    if (!al16(d.out) || d.ldo % 4 || d.o_stride % 4 || d.o_inner % 4 || (d.mask && !al16(d.mask)) ||
+        (d.res && !al16(d.res)))
+        return false;
+    // Split-k only as the reference allows it (matmul.rs:117-123): no epilogue
+    // but +=, out packed.
+    const bool can_split = !d.bias && !d.relu && !d.mask && !d.res && d.ldo == n && d.o_group == 1 &&
+                           (batch == 1 || d.o_stride == m * n);
+    // Output tile and split count by a rough time estimate: operand panels
+    // re-read from L2 per tile (~25 TB/s, stretched when fewer than 256
+    // workgroups run), plus the split partials written and summed (~5 TB/s).
+    struct Cfg {
+        int bm, bn;
+    };
+    const Cfg cands[] = {{128, 128}, {128, 64}, {64, 64}};
+    int best = -1;
+    int64_t best_splits = 1;
+    double best_t = 0;
+    for (int c = 0; c < 3; c++) {
+        const int bm = cands[c].bm, bn = cands[c].bn;
+        if (m % bm || n % bn) continue;
+        const int64_t tiles = batch * (m / bm) * (n / bn);
+        for (int64_t sp = 1; sp <= 32; sp *= 2) {
+            if (sp > 1 && (!can_split || k / sp < 4 * BK)) break;
+            const int64_t slice = cdiv(cdiv(k, sp), BK) * BK;
+            const int64_t splits = cdiv(k, slice);
+            const double wgs = (double)(tiles * splits);
+            double t = 4.0 * batch * m * n * k * (1.0 / bn + 1.0 / bm) / 25e12 * std::max(1.0, 256.0 / wgs);
+            if (splits > 1) t += 12.0 * splits * batch * m * n / 5e12 + 2e-6;
+            if (best < 0 || t < best_t) {
+                best = c;
+                best_splits = splits;
+                best_t = t;
+            }
+        }
+    }
+    if (best < 0) return false;
+    const int bm = cands[best].bm, bn = cands[best].bn;
+    const int64_t slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
+    const int64_t splits = cdiv(k, slice_k);
+    if (batch * splits > 65535 || m / bm > 65535 || n / bn > INT32_MAX) return false;
+
+    KArgs g;
+    std::memset(&g, 0, sizeof g);
+    g.a = d.a;
+    g.a_stride = d.a_stride;
+    g.a_group = d.a_group;
+    g.a_inner = d.a_inner;
+    g.lda = d.lda;
+    g.b = d.b;
+    g.b_stride = d.b_stride;
+    g.b_group = d.b_group;
+    g.b_inner = d.b_inner;
+    g.ldb = d.ldb;
+    g.out = d.out;
+    g.o_stride = d.o_stride;
+    g.o_group = d.o_group;
+    g.o_inner = d.o_inner;
+    g.ldo = d.ldo;
+    g.bias = d.bias;
+    g.bias_stride = d.bias_stride;
+    g.mask = d.mask;
+    g.res = d.res;
+    g.cs = d.cs;
+    g.cs_stride = d.cs_stride;
+    g.has_cs = d.has_cs;
+    g.relu = d.relu;
+    g.accumulate = d.accumulate;
+    g.m = (int32_t)m;
+    g.n = (int32_t)n;
+    g.k = (int32_t)k;
+    g.splits = (int32_t)splits;
+    g.slice_k = (int32_t)slice_k;
+    float *part = nullptr, *cs_part = nullptr;
+    if (splits > 1) {
+        const size_t pfl = (size_t)(batch * splits * m * n);
+        const size_t cfl = d.has_cs ? (size_t)(batch * splits * n) : 0;
+        part = static_cast<float *>(scratch(SCRATCH_SPLITK, sizeof(float) * (pfl + cfl)));
+        if (!part) {
+            *status = ST_ERR_OOM;
+            return true;
+        }
+        cs_part = part + pfl;
+        g.out = part;
+        g.cs = cs_part;
+    }
+    // Ring depths: 128 KB, 96 KB and 64 KB of LDS per workgroup.
+    KernelFn fn;
+    if (bm == 128 && bn == 128)
+        fn = pick2<128, 128, 4>(d.f16, d.ta, d.tb);
+    else if (bm == 128)
+        fn = pick2<128, 64, 4>(d.f16, d.ta, d.tb);
+    else
+        fn = pick2<64, 64, 4>(d.f16, d.ta, d.tb);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(n / bn), (unsigned)(m / bm), (unsigned)(batch * splits)), dim3(THREADS), 0,
+                       stream, g);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && splits > 1) {
+        const int64_t threads = batch * (m * n / 4) + (d.has_cs ? batch * n : 0);
+        hipLaunchKernelGGL(k_sum_slices, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, stream, part, d.out, m * n,
+                           (int32_t)splits, d.o_stride, batch, d.accumulate, d.has_cs ? cs_part : nullptr, d.cs,
+                           d.cs_stride, n);
+        e = hipGetLastError();
+    }
+    *status = e == hipSuccess ? ST_OK : fail(ST_ERR_HIP, "GEMM launch failed: %s", hipGetErrorString(e));
+    return true;
+}
+
+}  // namespace st
