@@ -69,13 +69,18 @@ def rel_err(got, want):
     return float(np.max(np.abs(got - want))) / max(scale, 1e-30)
 
 
-def run_case(dev, ci, case, use_f16):
+def run_case(dev, ci, case, use_f16, aligned16=False, packed=False):
+    """aligned16: every operand, stride and epilogue tensor on 16-byte boundaries (the layouts the
+    LDS-DMA kernel takes); packed: out matrices back to back (the layout split-k needs)."""
     batch, m, k, n, ta, tb, has_bias, relu, has_mask, has_res, acc = case
     rng = oracle.Rng(5 + ci)
     gauss = rng.gaussian
     aligned = use_f16 and ci % 2 == 1
     a_off, b_off, o_off, bias_off, m_off, r_off = 3, 5, (8 if aligned else 7), 2, 6, 1
     sa, sb, so = m * k + 1, (k * n + 2 if batch > 1 else 0), m * n + (0 if aligned else 3)
+    if aligned16:
+        a_off, b_off, o_off, bias_off, m_off, r_off = 4, 8, 12, 2, 16, 20
+        sa, sb, so = m * k + 4, (k * n + 8 if batch > 1 else 0), m * n + (0 if packed else 4)
     a = gauss(a_off + batch * sa)
     b = gauss(b_off + max(batch, 1) * max(sb, k * n))
     bias_stride = n + 1 if batch > 1 else 0
@@ -111,6 +116,29 @@ def run_case(dev, ci, case, use_f16):
     else:
         assert rel_err(got[body], want32[body]) <= 1e-5, what
         assert rel_err(got[cs], want32[cs]) <= 1e-4, what
+
+
+# Shapes for the LDS-DMA kernel (m, n tile-divisible, k % 32 == 0), run with 16-byte aligned
+# layouts: every epilogue term, batched strides, and split-k (few tiles, free epilogue) with
+# accumulate and column sums, batched and with many slices.
+# (batch, m, k, n, bias, relu, mask, residual, accumulate, packed)
+DMA_CASES = [
+    (2, 128, 96, 128, True, True, False, False, False, False),
+    (2, 128, 64, 64, True, False, True, True, True, False),
+    (1, 256, 128, 192, False, True, True, False, True, False),
+    (1, 256, 2048, 128, False, False, False, False, True, True),
+    (3, 64, 1024, 64, False, False, False, False, True, True),
+    (1, 64, 4096, 64, False, False, False, False, False, True),
+]
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+@pytest.mark.parametrize("tt", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("ci", range(len(DMA_CASES)))
+def test_matmul_aligned_layouts_match_oracle(dev, ci, tt, use_f16):
+    batch, m, k, n, bias, relu, mask, res, acc, packed = DMA_CASES[ci]
+    case = (batch, m, k, n, tt[0], tt[1], bias, relu, mask, res, acc)
+    run_case(dev, 100 + ci, case, use_f16, aligned16=True, packed=packed)
 
 
 @pytest.mark.parametrize("ci", range(len(CASES_F32)))
