@@ -46,7 +46,6 @@
 namespace {
 
 constexpr int D = 256;          // key width handled by the scan
-constexpr int DW = D / 16;      // code dwords per key
 constexpr int KMAX = 128;       // neighbours kept per query (knn.rs:21)
 constexpr int CAPW = 256;       // LDS candidate list per wave (entries)
 constexpr int PROBE_MAX = 16;   // most cells one query probes (ivf.rs:126)
@@ -180,8 +179,163 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// Query quantisation by one wave: qs = 2^(E-14) with max|q| = m 2^E,
+// Q = clamp(rint(q / qs), -16384, 16383).  Lane l writes Q of dims 4l .. 4l + 3
+// to sQ; every lane returns qs, |Q qs|^2 (from an exact sum of Q^2) and sum Q.
+struct QInfo {
+    float qs, qn;
+    int32_t sq;
+};
+
+__device__ __forceinline__ QInfo quantize_query(const float *qrow, int lane, int16_t *sQ) {
+    const float4 v = reinterpret_cast<const float4 *>(qrow)[lane];
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    const float mx = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+    float qs = 1.f, inv = 1.f;
+    if (mx > 0.f) {
+        int e;
+        frexpf(mx, &e);
+        qs = ldexpf(1.f, e - 14);
+        inv = ldexpf(1.f, 14 - e);
+    }
+    int32_t sq = 0;
+    double sq2 = 0.0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int32_t Q = (int32_t)fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16383.f);
+        sq += Q;
+        sq2 += (double)Q * (double)Q;
+        sQ[4 * lane + t] = (int16_t)Q;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        sq += __shfl_xor(sq, o, 64);
+        sq2 += __shfl_xor(sq2, o, 64);
+    }
+    return QInfo{qs, (float)sq2 * (qs * qs), sq};
+}
+
 typedef int32_t v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Matrix-core operands.  The key side (B, 128 x 16 per k-step, FP4 e2m1): a
+// code u kept in the low two bits of a nibble is the e2m1 number u / 2 (0, 0.5,
+// 1, 1.5), so w & 0x33333333 and (w >> 2) & 0x33333333 are ready operands:
+// nibble j of the first is code 2j of code dword w, of the second code 2j + 1.
+// Lane l supplies column l % 16 (a key) and the 32 values of k-block l / 16; at
+// k-step m (0, 1) they are dims 16 (4 (l/16) + 2m) + [0, 2, .., 14], then + 1,
+// then the same for code dword 4 (l/16) + 2m + 1: FP4 nibble n of k-block h is
+// k = 32 h + n.  The query side (A, FP8 e4m3) orders k differently: byte n of
+// lane group g is k = 16 g + n for n < 16 and k = 64 + 16 g + (n - 16) above.
+// Row 4s + p holds twice the balanced base-16 digit p of query slot s's Q
+// (Q = d0 + 16 d1 + 256 d2 + 4096 d3, d0..d2 in [-8, 7], d3 in [-4, 4]; 2d is
+// exact in FP8) at the dim its k pairs with; rows of absent slots are zero.
+// Row 4s + p of the product is then the integer sum_i d_p,i u_i, exact in the
+// f32 accumulator.  sQ holds nslot queries of D values each.
+__device__ __forceinline__ void build_aq(const int16_t *sQ, int nslot, int row, int col, v8i (&aq)[2]) {
+    const int slot = col >> 2, digit = col & 3;
+    const int16_t *Qs = sQ + (slot < nslot ? slot : 0) * D;
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+#pragma unroll
+        for (int v = 0; v < 8; v++) {
+            // elements 4v .. 4v + 3 of this lane's 32
+            float f[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = 4 * v + e;
+                const int k = n < 16 ? 16 * row + n : 64 + 16 * row + (n - 16);
+                const int nb = k & 31;
+                const int dword = 4 * (k >> 5) + 2 * m + (nb >> 4);
+                const int code = 2 * (nb & 7) + ((nb >> 3) & 1);
+                int32_t Q = Qs[16 * dword + code];
+                int32_t dgt = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int32_t d = p < 3 ? ((Q + 8) & 15) - 8 : Q;
+                    if (p == digit) dgt = d;
+                    Q = (Q - d) >> 4;
+                }
+                f[e] = slot < nslot ? (float)(2 * dgt) : 0.f;
+            }
+            int32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+            word = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], word, true);
+            aq[m][v] = word;
+        }
+    }
+}
+
+// 64 consecutive keys from row `base`: lane l holds bytes 16 (l/16) .. of key
+// 16G + l%16 for group G (the 16-byte key operand of matrix-core column l%16,
+// k-block l/16; a wave's load reads 1 KB of consecutive codes) and the scale of
+// key base + l.  Lanes lo <= l < hi carry keys of the scan; the rest are
+// ignored.  A store of fewer than 64 keys (SMALL) is read from base 0 with
+// each key index clamped to the store.
+struct Chunk {
+    uint4 c[4];
+    float sc;
+    int64_t base;
+    int32_t lo, hi, g;
+};
+
+template <bool SMALL>
+__device__ __forceinline__ void load_chunk(const uint8_t *codes, const float *scales, int64_t base, int64_t nrows,
+                                           int row, int col, int lane, Chunk &ch) {
+    const uint4 *cb = reinterpret_cast<const uint4 *>(codes + base * (D / 4));
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        int32_t kk = 16 * G + col;
+        if (SMALL) kk = kk < nrows ? kk : 0;
+        ch.c[G] = cb[kk * 4 + row];
+    }
+    ch.sc = scales[base + (SMALL ? (lane < nrows ? lane : 0) : lane)];
+}
+
+// Scores one chunk against up to 4 query slots: lane l ends with d[s] =
+// sum_i u_i Q_s,i and n12 = #{i: u_i in {1, 2}} for key base + l.
+__device__ __forceinline__ void score_chunk(const Chunk &ch, const v8i (&aq)[2], int32_t (&d)[4], int32_t &n12) {
+    int32_t vg[4], pc[4];
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        const uint32_t w[4] = {ch.c[G].x, ch.c[G].y, ch.c[G].z, ch.c[G].w};
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const v8i bk = {(int32_t)(w[2 * m] & 0x33333333u), (int32_t)((w[2 * m] >> 2) & 0x33333333u),
+                            (int32_t)(w[2 * m + 1] & 0x33333333u), (int32_t)((w[2 * m + 1] >> 2) & 0x33333333u),
+                            0, 0, 0, 0};
+            // A: FP8 e4m3 (cbsz 0), B: FP4 e2m1 (blgp 4), unit block scales (E8M0 127).
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aq[m], bk, acc, 0, 4, 0, 127, 0, 127);
+        }
+        // Lane group s holds rows 4s .. 4s + 3 (slot s's digit sums) in
+        // registers 0..3; sum u Q = sum_p 16^p (row 4s + p), every step an
+        // exact integer.
+        const float dq = __builtin_fmaf(16.f, __builtin_fmaf(16.f, __builtin_fmaf(16.f, acc[3], acc[2]), acc[1]),
+                                        acc[0]);
+        vg[G] = (int32_t)dq;
+        // Codes with u in {1, 2} of key 16G + col among this lane's 64 dims.
+        int32_t p = 0;
+#pragma unroll
+        for (int s = 0; s < 4; s++) p += __popc((w[s] ^ (w[s] >> 1)) & 0x55555555u);
+        pc[G] = p;
+    }
+    // vg[G] in lane group s is slot s's dot of key 16G + col: transpose the
+    // 4 x 4 (register, lane group) blocks so that d[s] in lane group G holds
+    // it (lane l ends with key l's dots); sum group G's counts over the four
+    // lane groups into lane group G.
+    auto a = __builtin_amdgcn_permlane32_swap((unsigned)vg[0], (unsigned)vg[2], false, false);
+    auto b = __builtin_amdgcn_permlane32_swap((unsigned)vg[1], (unsigned)vg[3], false, false);
+    auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    auto e = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    d[0] = (int32_t)c[0];
+    d[1] = (int32_t)c[1];
+    d[2] = (int32_t)e[0];
+    d[3] = (int32_t)e[1];
+    auto x = __builtin_amdgcn_permlane32_swap((unsigned)pc[0], (unsigned)pc[2], false, false);
+    auto y = __builtin_amdgcn_permlane32_swap((unsigned)pc[1], (unsigned)pc[3], false, false);
+    auto z = __builtin_amdgcn_permlane16_swap(x[0] + x[1], y[0] + y[1], false, false);
+    n12 = (int32_t)(z[0] + z[1]);
+}
 
 constexpr int E8 = KMAX / SW;  // each wave's published rank: SW * E8 = KMAX keys
 
@@ -207,35 +361,11 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     const int64_t q = blockIdx.x;
 
     if (wave == 0) {
-        // Query quantisation: qs = 2^(E-14) with max|q| = m 2^E, Q = clamp(rint(q / qs), -16384, 16383).
-        const float4 v = reinterpret_cast<const float4 *>(queries + q * D)[lane];
-        const float x[4] = {v.x, v.y, v.z, v.w};
-        const float mx = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
-        float qs = 1.f, inv = 1.f;
-        if (mx > 0.f) {
-            int e;
-            frexpf(mx, &e);
-            qs = ldexpf(1.f, e - 14);
-            inv = ldexpf(1.f, 14 - e);
-        }
-        int32_t sq = 0;
-        double sq2 = 0.0;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int32_t Q = (int32_t)fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16383.f);
-            sq += Q;
-            sq2 += (double)Q * (double)Q;
-            s_Q[4 * lane + t] = (int16_t)Q;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            sq += __shfl_xor(sq, o, 64);
-            sq2 += __shfl_xor(sq2, o, 64);
-        }
+        const QInfo qi = quantize_query(queries + q * D, lane, s_Q);
         if (lane == 0) {
-            s_qs = qs;
-            s_qn = (float)sq2 * (qs * qs);
-            s_sq = sq;
+            s_qs = qi.qs;
+            s_qn = qi.qn;
+            s_sq = qi.sq;
         }
     } else if (wave == 1) {
         // The probed cells and their row ranges (all loads in flight together);
@@ -300,50 +430,9 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     }
     __syncthreads();
 
-    // Matrix-core operands.  The key side (B, 128 x 16 per k-step, FP4 e2m1):
-    // a code u kept in the low two bits of a nibble is the e2m1 number u / 2
-    // (0, 0.5, 1, 1.5), so w & 0x33333333 and (w >> 2) & 0x33333333 are ready
-    // operands: nibble j of the first is code 2j of code dword w, of the
-    // second code 2j + 1.  Lane l supplies column l % 16 (a key) and the 32
-    // values of k-block l / 16; at k-step m (0, 1) they are dims
-    // 16 (4 (l/16) + 2m) + [0, 2, .., 14], then + 1, then the same for code
-    // dword 4 (l/16) + 2m + 1: FP4 nibble n of k-block h is k = 32 h + n.  The
-    // query side (A, FP8 e4m3) orders k differently: byte n of lane group g is
-    // k = 16 g + n for n < 16 and k = 64 + 16 g + (n - 16) above.  Row p < 4
-    // holds twice the balanced base-16 digit p of Q (Q = d0 + 16 d1 + 256 d2 +
-    // 4096 d3, d0..d2 in [-8, 7], d3 in [-4, 4]; 2d is exact in FP8) at the dim
-    // its k pairs with; rows 4..15 are zero.  Row p of the product is then the
-    // integer sum_i d_p,i u_i, exact in the f32 accumulator.
     const int row = lane >> 4, col = lane & 15;
     v8i aq[2];
-#pragma unroll
-    for (int m = 0; m < 2; m++) {
-#pragma unroll
-        for (int v = 0; v < 8; v++) {
-            // elements 4v .. 4v + 3 of this lane's 32
-            float f[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int n = 4 * v + e;
-                const int k = n < 16 ? 16 * row + n : 64 + 16 * row + (n - 16);
-                const int nb = k & 31;
-                const int dword = 4 * (k >> 5) + 2 * m + (nb >> 4);
-                const int code = 2 * (nb & 7) + ((nb >> 3) & 1);
-                int32_t Q = s_Q[16 * dword + code];
-                int32_t dgt = 0;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int32_t d = p < 3 ? ((Q + 8) & 15) - 8 : Q;
-                    if (p == col) dgt = d;
-                    Q = (Q - d) >> 4;
-                }
-                f[e] = col < 4 ? (float)(2 * dgt) : 0.f;
-            }
-            int32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
-            word = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], word, true);
-            aq[m][v] = word;
-        }
-    }
+    build_aq(s_Q, 1, row, col, aq);
     const float qs = s_qs;
     const int32_t sq = s_sq;
     const int np = s_np;
@@ -355,22 +444,10 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     // shared counter, so each wave's chunks come in increasing order and a fast
     // wave simply scans more of them (a chunk is the up to 64 keys of one cell
     // at rows row0 .. row0 + nk; the chunk -> (cell, row) map is uniform per
-    // wave).  A chunk is read as the 64
-    // keys from base = min(row0, nrows - 64), so the loads of a chunk are four
-    // fixed offsets from one address and never leave the store; lane l scores
-    // key base + l and keeps it when lo <= l < hi.  For group G (keys 16G ..
-    // 16G + 15 of the 64) lane l loads bytes 16 (l/16) .. of key 16G + l%16:
-    // the 16-byte key operand of matrix-core column l%16, k-block l/16, for the
-    // four k-steps; a wave's load reads 1 KB of consecutive codes.  A store of
-    // fewer than 64 keys (SMALL) is read from base 0 with each key index
-    // clamped to the store.
+    // wave).  A chunk is read as the 64 keys from base = min(row0, nrows - 64),
+    // so the loads of a chunk are four fixed offsets from one address and
+    // never leave the store.
     int ccell = 0;
-    struct Chunk {
-        uint4 c[4];
-        float sc;
-        int64_t base;
-        int32_t lo, hi, g;
-    };
     int32_t c0 = 0;
     while (c0 < np - 1 && s_cpre[c0 + 1] == 0) c0++;
     const int64_t safe_row0 = nchunks > 0 ? s_r0[c0] : 0;
@@ -389,14 +466,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         ch.base = base;
         ch.lo = (int32_t)(row0 - base);
         ch.hi = ch.lo + nk;
-        const uint4 *cb = reinterpret_cast<const uint4 *>(codes + base * (D / 4));
-#pragma unroll
-        for (int G = 0; G < 4; G++) {
-            int32_t kk = 16 * G + col;
-            if (SMALL) kk = kk < nrows ? kk : 0;
-            ch.c[G] = cb[kk * 4 + row];
-        }
-        ch.sc = scales[base + (SMALL ? (lane < nrows ? lane : 0) : lane)];  // lane l scores key base + l
+        load_chunk<SMALL>(codes, scales, base, nrows, row, col, lane, ch);
     };
 
     // Each wave keeps its own candidate list (no workgroup barrier in the scan,
@@ -433,43 +503,9 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         refresh();
     };
     auto score = [&](const Chunk &ch) {
-        int32_t vg[4], pc[4];
-#pragma unroll
-        for (int G = 0; G < 4; G++) {
-            const uint32_t w[4] = {ch.c[G].x, ch.c[G].y, ch.c[G].z, ch.c[G].w};
-            v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int m = 0; m < 2; m++) {
-                const v8i bk = {(int32_t)(w[2 * m] & 0x33333333u), (int32_t)((w[2 * m] >> 2) & 0x33333333u),
-                                (int32_t)(w[2 * m + 1] & 0x33333333u), (int32_t)((w[2 * m + 1] >> 2) & 0x33333333u),
-                                0, 0, 0, 0};
-                // A: FP8 e4m3 (cbsz 0), B: FP4 e2m1 (blgp 4), unit block scales (E8M0 127).
-                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aq[m], bk, acc, 0, 4, 0, 127, 0, 127);
-            }
-            // Rows 0..3 (registers 0..3 of row-0 lanes, zero in other lanes) hold
-            // sum d_p u; sum u Q = sum_p 16^p (row p), every step an exact integer.
-            const float dq = __builtin_fmaf(16.f, __builtin_fmaf(16.f, __builtin_fmaf(16.f, acc[3], acc[2]), acc[1]),
-                                            acc[0]);
-            vg[G] = (int32_t)dq;
-            // Codes with u in {1, 2} of key 16G + col among this lane's 64 dims.
-            int32_t p = 0;
-#pragma unroll
-            for (int s = 0; s < 4; s++) p += __popc((w[s] ^ (w[s] >> 1)) & 0x55555555u);
-            pc[G] = p;
-        }
-        // Route group G's dot (in row 0) to row G and sum group G's counts over
-        // the four rows into row G: lane l ends with key l's dot and count.
-        int32_t duq, n12;
-        {
-            auto a = __builtin_amdgcn_permlane32_swap((unsigned)vg[0], (unsigned)vg[2], false, false);
-            auto b = __builtin_amdgcn_permlane32_swap((unsigned)vg[1], (unsigned)vg[3], false, false);
-            auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-            duq = (int32_t)c[0];
-            auto x = __builtin_amdgcn_permlane32_swap((unsigned)pc[0], (unsigned)pc[2], false, false);
-            auto y = __builtin_amdgcn_permlane32_swap((unsigned)pc[1], (unsigned)pc[3], false, false);
-            auto z = __builtin_amdgcn_permlane16_swap(x[0] + x[1], y[0] + y[1], false, false);
-            n12 = (int32_t)(z[0] + z[1]);
-        }
+        int32_t dq[4], n12;
+        score_chunk(ch, aq, dq, n12);
+        const int32_t duq = dq[0];
         const float sc = ch.sc;
         const int32_t dot = 2 * duq - 3 * sq;
         const int32_t c2 = c2_base - 8 * n12;
@@ -636,8 +672,9 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     if (nq == 0) return ST_OK;
     if (nq > INT32_MAX / PROBE_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many queries for one call");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
-    hipLaunchKernelGGL(k_search, dim3((unsigned)nq), dim3(STH), 0, st::stream_of(stream), codes, scales, cell_start,
-                       ncells, queries, probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist);
+    const hipStream_t s = st::stream_of(stream);
+    hipLaunchKernelGGL(k_search, dim3((unsigned)nq), dim3(STH), 0, s, codes, scales, cell_start, ncells, queries,
+                       probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist);
     ST_LAUNCH_CHECK();
     return ST_OK;
 }

@@ -89,6 +89,32 @@ def test_search_stores_near_one_chunk(dev, sizes):
         check_search(dev, store, codes, scales, cs, queries, probes, k)
 
 
+def test_search_many_cells_and_sixteen_probes(dev):
+    # 20000 cells of 0..4 keys, 16 probes (the most a query may have), one repeated.
+    rng = np.random.default_rng(21)
+    ncells = 20000
+    sizes = rng.integers(0, 5, ncells)
+    store, codes, scales, cs = make_store(dev, sizes, 23)
+    nq = 24
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, 16, replace=False) for _ in range(nq)]).astype(np.int32)
+    probes[0, 3] = probes[0, 9]
+    for k in (128, 5):
+        check_search(dev, store, codes, scales, cs, queries, probes, k)
+
+
+def test_search_many_queries_sharing_cells(dev):
+    # 600 queries x 8 probes over 100 cells: every cell is probed by ~48 queries.
+    rng = np.random.default_rng(31)
+    ncells = 100
+    sizes = rng.integers(60, 140, ncells)
+    store, codes, scales, cs = make_store(dev, sizes, 33)
+    nq = 600
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, 8, replace=False) for _ in range(nq)]).astype(np.int32)
+    check_search(dev, store, codes, scales, cs, queries, probes, 128)
+
+
 def test_search_ties_break_by_key_index(dev):
     # Identical keys give identical scores: the kept ones must be the lowest indices.
     base = np.random.default_rng(4).standard_normal(D).astype(np.float32)
