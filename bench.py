@@ -2,8 +2,11 @@
 
 One step = one pass of the d_model-256 byte-LM training-step GEMM set
 (T = 4096 tokens, 5 layers x {forward, dX, dW} = 15 GEMMs, 20,937,965,568 FLOP)
-on the f16-in/f32-accumulate route, replayed from a HIP graph.  `value` is that
-set's TFLOP/s.  The same JSON line carries the other configurations measured in
+on the f16-in/f32-accumulate route, issued as one grouped call
+(st_matmul_grouped: the 15 GEMMs are independent here) and replayed from a HIP
+graph.  `value` is that set's TFLOP/s; the same set issued in training-step
+order (forward one by one, each layer's dW and dX grouped) and one call per
+GEMM are reported beside it.  The same JSON line carries the other configurations measured in
 the same run (256^3 f32, the tape backward forms, the f32 step set, batched
 causal attention, the 125M-key 2-bit kNN scan), a roofline for the dominant
 kernel of each headline, and the CPU baseline (the oracle's restatement of the
@@ -73,19 +76,22 @@ def traffic_for(kernel_key, src_rel):
     return int(e["fetch_bytes"] + e["write_bytes"])
 
 
-def roofline(kernel, flops, nbytes, ms, traffic=None):
-    """Roofline entry for one kernel: the binding roof is the lower of MFMA peak and intensity x HBM peak."""
+def roofline(kernel, flops, nbytes, ms, traffic=None, route="f16"):
+    """Roofline entry for one kernel: the binding roof is the lower of the route's MFMA peak and intensity x HBM
+    peak."""
     tflops = flops / ms / 1e9
     gbs = nbytes / ms / 1e6
-    ridge = PEAK["f16"] * 1e12 / (PEAK["hbm_gbs"] * 1e9)
+    peak = PEAK[route]
+    ridge = peak * 1e12 / (PEAK["hbm_gbs"] * 1e9)
     if flops / nbytes < ridge:
         r = dict(kernel=kernel, bound="hbm", achieved=round(gbs, 1), peak=PEAK["hbm_gbs"], unit="GB/s",
                  frac=round(gbs / PEAK["hbm_gbs"], 4))
     else:
-        r = dict(kernel=kernel, bound="mfma", achieved=round(tflops, 2), peak=PEAK["f16"], unit="TFLOP/s",
-                 frac=round(tflops / PEAK["f16"], 4))
+        r = dict(kernel=kernel, bound="mfma", achieved=round(tflops, 2), peak=peak, unit="TFLOP/s",
+                 frac=round(tflops / peak, 4))
     r.update(traffic=traffic, algorithmic_bytes=int(nbytes), flops=int(flops), ms=round(ms, 5),
-             tflops=round(tflops, 2), mfma_frac=round(tflops / PEAK["f16"], 4), hbm_gbs=round(gbs, 1))
+             tflops=round(tflops, 2), mfma_frac=round(tflops / peak, 4), hbm_gbs=round(gbs, 1),
+             roof_tflops=round(min(peak, flops / nbytes * PEAK["hbm_gbs"] / 1e3), 1))
     return r
 
 
@@ -160,6 +166,7 @@ class StepSet:
         return lambda: st.matmul_with(A, B, O, 1, m, k, n, None, use_f16)
 
     def step_fn(self, use_f16):
+        """The 15 GEMMs one call each (the reference's dispatch pattern), in set order."""
         fns = [self.call_fn(i, use_f16) for i in range(len(self.calls))]
 
         def step():
@@ -167,17 +174,51 @@ class StepSet:
                 f()
         return step
 
+    def args(self, i, use_f16):
+        import scratchtape_amd as st
+        _, a, b, o, m, k, n = self.calls[i]
+        return (st.MatRef(**a), st.MatRef(**b), st.MatRef(**o), 1, m, k, n, None, use_f16)
+
+    def grouped_fn(self, use_f16):
+        """The 15 GEMMs as one st_matmul_grouped call (they are independent here)."""
+        import scratchtape_amd as st
+        calls = [self.args(i, use_f16) for i in range(len(self.calls))]
+        return lambda: st.matmul_grouped(calls)
+
+    def step_order_fn(self, use_f16):
+        """The order a training step can issue them in: the 5 forward GEMMs one by one (each needs the layer
+        before), then per layer from the head down one grouped call of its dW and dX (gpu_step/tape.rs:324-347)."""
+        import scratchtape_amd as st
+        fwd = [self.call_fn(3 * l, use_f16) for l in range(len(LAYERS))]
+        bwd = [[self.args(3 * l + 2, use_f16), self.args(3 * l + 1, use_f16)] for l in reversed(range(len(LAYERS)))]
+
+        def step():
+            for f in fwd:
+                f()
+            for pair in bwd:
+                st.matmul_grouped(pair)
+        return step
+
 
 def bench_gemm_set(dev, stream, steps, warmup, use_f16):
+    """Times the set three ways: one grouped call (the headline), step order (forward one by one, backward
+    pairs grouped) and one call per GEMM; each eager (HIP events around the calls) and as a HIP graph."""
     import torch
     ss = StepSet(dev)
-    step = ss.step_fn(use_f16)
+    modes = {"grouped": ss.grouped_fn(use_f16), "step_order": ss.step_order_fn(use_f16),
+             "serial": ss.step_fn(use_f16)}
+    times = {}
     with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            step()
+        for name, fn in modes.items():
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            eager = time_events(fn, steps, stream)
+            graph, _ = time_graph(fn, steps, warmup, stream)
+            times[name] = dict(eager_ms=round(eager, 5), graph_ms=round(graph, 5),
+                               tflops=round(ss.flops / graph / 1e9, 2))
+        modes["grouped"]()  # the outputs the parity check reads come from the grouped launch
         torch.cuda.synchronize()
-        eager_ms = time_events(step, steps, stream)
-        graph_ms, _ = time_graph(step, steps, warmup, stream)
         per_call = []
         for i, (label, _, _, _, m, k, n) in enumerate(ss.calls):
             f = ss.call_fn(i, use_f16)
@@ -186,8 +227,9 @@ def bench_gemm_set(dev, stream, steps, warmup, use_f16):
             fl = 2 * m * k * n
             per_call.append(dict(gemm=label, m=m, k=k, n=n, ms=round(ms, 5), tflops=round(fl / ms / 1e9, 2),
                                  gbs=round(4 * (m * k + k * n + m * n) / ms / 1e6, 1)))
+    modes["grouped"]()
     torch.cuda.synchronize()
-    return ss, eager_ms, graph_ms, per_call
+    return ss, times, per_call
 
 
 def check_gemm_set(ss, use_f16, which=(2, 5, 8)):
@@ -440,30 +482,33 @@ def main():
 
     if args.only in ("all", "gemm"):
         log("[bench] C3 step GEMM set, f16-in/f32-acc")
-        ss16, eager16, graph16, calls16 = bench_gemm_set(dev, stream, args.steps, args.warmup, True)
+        ss16, t16, calls16 = bench_gemm_set(dev, stream, args.steps, args.warmup, True)
         err16 = check_gemm_set(ss16, True)
-        log(f"[bench] f16 set: graph {graph16:.4f} ms, eager {eager16:.4f} ms, parity {err16:.2e}")
+        log(f"[bench] f16 set: {t16}, parity {err16:.2e}")
         log("[bench] C3 step GEMM set, f32")
-        ss32, eager32, graph32, calls32 = bench_gemm_set(dev, stream, args.steps, args.warmup, False)
+        ss32, t32, calls32 = bench_gemm_set(dev, stream, args.steps, args.warmup, False)
         err32 = check_gemm_set(ss32, False)
-        log(f"[bench] f32 set: graph {graph32:.4f} ms, eager {eager32:.4f} ms, parity {err32:.2e}")
+        log(f"[bench] f32 set: {t32}, parity {err32:.2e}")
         if err16 > 1e-5 or err32 > 1e-5:
             log("[bench] PARITY FAILURE: refusing to report")
             sys.exit(3)
-        dom = max(calls16, key=lambda c: c["ms"])
+        graph16 = t16["grouped"]["graph_ms"]
         value = ss16.flops / graph16 / 1e9
-        dm, dk, dn = dom["m"], dom["k"], dom["n"]
-        roof = roofline(f"k_gemm f16 ({dom['gemm']}: {dm}x{dk}x{dn})", 2 * dm * dk * dn,
-                        4 * (dm * dk + dk * dn + dm * dn), dom["ms"],
-                        traffic_for(f"k_gemm f16 {dom['gemm']}", "scratchtape_amd/csrc/gemm.hip"))
-        extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes, graph_ms=round(graph16, 5),
-                                   eager_ms=round(eager16, 5), tflops=round(value, 2),
-                                   mfma_frac=round(value / PEAK["f16"], 4),
-                                   hbm_gbs=round(ss16.bytes / graph16 / 1e6, 1), per_gemm=calls16,
+        # The dominant kernel is the grouped launch itself (k_gemm_group, plus the split-k sum k_sum_group):
+        # the set's flops and algorithmic bytes over its per-call time from HIP events on its stream.
+        roof = roofline("k_gemm_group f16 (+ k_sum_group): the 15-GEMM set in one grouped call", ss16.flops,
+                        ss16.bytes, t16["grouped"]["eager_ms"],
+                        traffic_for("k_gemm_group f16 step set", "scratchtape_amd/csrc/gemm_group.hip"))
+        extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes, graph_ms=graph16,
+                                   tflops=round(value, 2), mfma_frac=round(value / PEAK["f16"], 4),
+                                   hbm_gbs=round(ss16.bytes / graph16 / 1e6, 1), modes=t16, per_gemm=calls16,
                                    parity_max_rel_err=err16)
-        v32 = ss32.flops / graph32 / 1e9
-        extra["c3_f32_set"] = dict(graph_ms=round(graph32, 5), eager_ms=round(eager32, 5), tflops=round(v32, 2),
-                                   mfma_frac=round(v32 / PEAK["f32"], 4), per_gemm=calls32, parity_max_rel_err=err32)
+        g32 = t32["grouped"]["graph_ms"]
+        v32 = ss32.flops / g32 / 1e9
+        extra["c3_f32_set"] = dict(graph_ms=g32, tflops=round(v32, 2), mfma_frac=round(v32 / PEAK["f32"], 4),
+                                   roofline=roofline("k_gemm_group f32 (+ k_sum_group)", ss32.flops, ss32.bytes,
+                                                     t32["grouped"]["eager_ms"], route="f32"),
+                                   modes=t32, per_gemm=calls32, parity_max_rel_err=err32)
         log("[bench] C1 / C2 tape forms")
         extra["c1_256cube_f32"] = bench_tape_forms(dev, stream, 256, 256, 256, False)
         extra["c2_backward_f32"] = bench_tape_forms(dev, stream, 4096, 256, 1024, False)

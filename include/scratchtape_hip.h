@@ -98,6 +98,28 @@ st_status st_matmul_with(const st_matref *a, const st_matref *b, const st_matref
                          int64_t batch, int64_t m, int64_t k, int64_t n, const st_epilogue *epi,
                          int32_t use_f16, st_stream stream);
 
+/* One GEMM of st_matmul_grouped: the arguments of st_matmul_with (an
+ * all-zero epi is no epilogue). */
+typedef struct st_gemm {
+    st_matref a, b, out;
+    st_epilogue epi;
+    int64_t batch, m, k, n;
+    int32_t use_f16;
+    int32_t reserved;
+} st_gemm;
+
+/* GEMMs the reference issues back to back on its queue that do not depend on
+ * each other, e.g. a Linear backward's dW = x^T dz (+ column sums) and
+ * dx = dz W^T (gpu_step/tape.rs:324-347), as st_matmul_with each: no GEMM
+ * of the group may read or write memory that another one writes.  Those that
+ * tile by 128 x 128 (m % 128 == 0, n % 128 == 0, k % 32 == 0, k >= 128,
+ * 16-byte aligned operands) run as one persistent launch per route (f16,
+ * f32; up to 16 GEMMs per launch), the rest one by one.  Per element the
+ * result equals st_matmul_with's, except that split-k may split k at other
+ * points (the same fixed-order sum, other partial sums).  Uses the split-k
+ * scratch arena: serialise on one stream per device. */
+st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_stream stream);
+
 /* gpu_step/matmul.rs:97-102 `f16_enabled`: 1 unless the environment sets
  * TRAIN_F16=0 (gfx950 always has f16 x f16 -> f32 matrix cores).  Read once. */
 int32_t st_f16_enabled(void);

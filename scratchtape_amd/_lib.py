@@ -44,6 +44,11 @@ class StEpilogue(ctypes.Structure):
                 ("has_col_sum", _i32), ("reserved", _i32), ("col_sum_off", _i64), ("col_sum_stride", _i64)]
 
 
+class StGemm(ctypes.Structure):
+    _fields_ = [("a", StMatRef), ("b", StMatRef), ("out", StMatRef), ("epi", StEpilogue), ("batch", _i64),
+                ("m", _i64), ("k", _i64), ("n", _i64), ("use_f16", _i32), ("reserved", _i32)]
+
+
 _R = ctypes.POINTER(StMatRef)
 _E = ctypes.POINTER(StEpilogue)
 
@@ -52,6 +57,7 @@ SIGNATURES = {
     "st_matmul": [_R, _R, _R, _i64, _i64, _i64, _i64, _E, _vp],
     "st_matmul_f32": [_R, _R, _R, _i64, _i64, _i64, _i64, _E, _vp],
     "st_matmul_with": [_R, _R, _R, _i64, _i64, _i64, _i64, _E, _i32, _vp],
+    "st_matmul_grouped": [ctypes.POINTER(StGemm), _i64, _vp],
     "st_f16_enabled": [],
     "st_ndarray_matmul": [_vp, _vp, _vp, _i64, _i64, _i64],
     "st_softmax": [_vp, _vp, _i64, _i64, _i64, _f32, _i32, _i32, _vp],

@@ -31,7 +31,9 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 #include "gemm_dma.h"
@@ -420,27 +422,77 @@ st_status check_ref(const st_matref *r, const char *what) {
     return ST_OK;
 }
 
-st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
-                    int64_t k, int64_t n, const st_epilogue *epi_in, bool use_f16, hipStream_t stream) {
-    st::clear_error();
+// The reference's argument checks for one call (its assert!s).
+st_status check_call(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
+                     int64_t k, int64_t n) {
     st_status s;
     if ((s = check_ref(a, "a")) || (s = check_ref(b, "b")) || (s = check_ref(out, "out"))) return s;
     if (out->trans) return st::fail(ST_ERR_INVALID, "out is stored row-major");
     if (batch < 0 || m < 0 || k < 0 || n < 0) return st::fail(ST_ERR_INVALID, "negative batch or shape");
     if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2)
         return st::fail(ST_ERR_INVALID, "matrix dimension too large");
+    return ST_OK;
+}
+
+// The reference's f16 eligibility (matmul.rs:108-112, 524-534): k % 32, m % 64
+// and n % 64 (or n % 32 for its 64x32 tile), and not column sums of a
+// transposed b.
+bool f16_route(bool use_f16, const st_epilogue &epi, const st_matref *b, int64_t m, int64_t k, int64_t n) {
+    return use_f16 && !(epi.has_col_sum && b->trans) && k > 0 && k % 32 == 0 && m % 64 == 0 && n % 32 == 0;
+}
+
+// One call as the LDS-DMA kernels take it: element offsets folded into the
+// pointers, group 0 read as 1, packed leading dimensions made explicit.
+st::DmaGemm make_dma(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
+                     int64_t k, int64_t n, const st_epilogue &epi, bool f16) {
+    st::DmaGemm d;
+    std::memset(&d, 0, sizeof d);
+    d.a = a->p + a->off;
+    d.a_stride = a->stride;
+    d.a_group = a->group > 0 ? a->group : 1;
+    d.a_inner = a->inner;
+    d.lda = a->ld ? a->ld : (a->trans ? m : k);
+    d.ta = a->trans != 0;
+    d.b = b->p + b->off;
+    d.b_stride = b->stride;
+    d.b_group = b->group > 0 ? b->group : 1;
+    d.b_inner = b->inner;
+    d.ldb = b->ld ? b->ld : (b->trans ? k : n);
+    d.tb = b->trans != 0;
+    d.out = out->p + out->off;
+    d.o_stride = out->stride;
+    d.o_group = out->group > 0 ? out->group : 1;
+    d.o_inner = out->inner;
+    d.ldo = out->ld ? out->ld : n;
+    d.bias = epi.bias ? epi.bias + epi.bias_off : nullptr;
+    d.bias_stride = epi.bias_stride;
+    d.mask = epi.mask ? epi.mask + epi.mask_off : nullptr;
+    d.res = epi.residual ? epi.residual + epi.residual_off : nullptr;
+    d.cs = out->p + epi.col_sum_off;
+    d.cs_stride = epi.col_sum_stride;
+    d.has_cs = epi.has_col_sum;
+    d.relu = epi.relu;
+    d.accumulate = epi.accumulate;
+    d.f16 = f16;
+    d.batch = batch;
+    d.m = m;
+    d.k = k;
+    d.n = n;
+    return d;
+}
+
+st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
+                    int64_t k, int64_t n, const st_epilogue *epi_in, bool use_f16, hipStream_t stream) {
+    st::clear_error();
+    st_status s;
+    if ((s = check_call(a, b, out, batch, m, k, n))) return s;
     st_epilogue epi;
     std::memset(&epi, 0, sizeof epi);
     if (epi_in) epi = *epi_in;
     if (batch == 0 || m == 0 || n == 0) return ST_OK;
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
 
-    // The reference's f16 eligibility (matmul.rs:108-112, 524-534): k % 32,
-    // m % 64 and n % 64 (or n % 32 for its 64x32 tile), and not column sums
-    // of a transposed b.
-    const bool f16 = use_f16 && !(epi.has_col_sum && b->trans) && k > 0 && k % 32 == 0 && m % 64 == 0 &&
-                     n % 32 == 0;
-
+    const bool f16 = f16_route(use_f16, epi, b, m, k, n);
     const int64_t ag = a->group > 0 ? a->group : 1, bg = b->group > 0 ? b->group : 1;
     const int64_t og = out->group > 0 ? out->group : 1;
     const int64_t lda = a->ld ? a->ld : (a->trans ? m : k);
@@ -449,41 +501,8 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
 
     // Tile-divisible, 16-byte aligned problems run on the LDS-DMA kernel.
     {
-        st::DmaGemm d;
-        std::memset(&d, 0, sizeof d);
-        d.a = a->p + a->off;
-        d.a_stride = a->stride;
-        d.a_group = ag;
-        d.a_inner = a->inner;
-        d.lda = lda;
-        d.ta = a->trans != 0;
-        d.b = b->p + b->off;
-        d.b_stride = b->stride;
-        d.b_group = bg;
-        d.b_inner = b->inner;
-        d.ldb = ldb;
-        d.tb = b->trans != 0;
-        d.out = out->p + out->off;
-        d.o_stride = out->stride;
-        d.o_group = og;
-        d.o_inner = out->inner;
-        d.ldo = ldo;
-        d.bias = epi.bias ? epi.bias + epi.bias_off : nullptr;
-        d.bias_stride = epi.bias_stride;
-        d.mask = epi.mask ? epi.mask + epi.mask_off : nullptr;
-        d.res = epi.residual ? epi.residual + epi.residual_off : nullptr;
-        d.cs = out->p + epi.col_sum_off;
-        d.cs_stride = epi.col_sum_stride;
-        d.has_cs = epi.has_col_sum;
-        d.relu = epi.relu;
-        d.accumulate = epi.accumulate;
-        d.f16 = f16;
-        d.batch = batch;
-        d.m = m;
-        d.k = k;
-        d.n = n;
         st_status ds = ST_OK;
-        if (st::gemm_dma(d, stream, &ds)) return ds;
+        if (st::gemm_dma(make_dma(a, b, out, batch, m, k, n, epi, f16), stream, &ds)) return ds;
     }
 
     TileCfg tc = choose_tile(batch, m, n);
@@ -601,6 +620,56 @@ extern "C" st_status st_matmul_with(const st_matref *a, const st_matref *b, cons
                                     int64_t batch, int64_t m, int64_t k, int64_t n, const st_epilogue *epi,
                                     int32_t use_f16, st_stream stream) {
     return gemm_impl(a, b, out, batch, m, k, n, epi, use_f16 != 0, st::stream_of(stream));
+}
+
+extern "C" st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_stream stream) {
+    st::clear_error();
+    if (count < 0 || (count > 0 && !gemms)) return st::fail(ST_ERR_INVALID, "grouped GEMM: bad count or NULL array");
+    for (int64_t i = 0; i < count; i++) {
+        const st_gemm &g = gemms[i];
+        const st_status s = check_call(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n);
+        if (s) {
+            const std::string msg = st_last_error();
+            return st::fail(s, "GEMM %lld of the group: %s", (long long)i, msg.c_str());
+        }
+    }
+    if (count == 0) return ST_OK;
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    const hipStream_t s = st::stream_of(stream);
+    std::vector<st::DmaGemm> elig[2];  // by route (f32, f16)
+    std::vector<int64_t> rest;
+    for (int64_t i = 0; i < count; i++) {
+        const st_gemm &g = gemms[i];
+        if (g.batch == 0 || g.m == 0 || g.n == 0) continue;
+        const bool f16 = f16_route(g.use_f16 != 0, g.epi, &g.b, g.m, g.k, g.n);
+        const st::DmaGemm d = make_dma(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n, g.epi, f16);
+        if (st::group_eligible(d))
+            elig[f16 ? 1 : 0].push_back(d);
+        else
+            rest.push_back(i);
+    }
+    // 256-row tiles only when the route's GEMMs give every CU at least one of
+    // them; a small group (a single Linear backward) keeps 128-row tiles.
+    std::vector<st::DmaGemm> grp[4];  // route + 2 * (256-row tiles)
+    for (int f = 0; f < 2; f++) {
+        int64_t tall_tiles = 0;
+        for (const st::DmaGemm &d : elig[f])
+            if (st::group_tall(d)) tall_tiles += d.batch * (d.m / 256) * (d.n / 128);
+        const bool use_tall = tall_tiles >= 256;
+        for (const st::DmaGemm &d : elig[f]) grp[f + 2 * (use_tall && st::group_tall(d))].push_back(d);
+    }
+    for (int f = 0; f < 4; f++)
+        for (size_t c = 0; c < grp[f].size(); c += st::GROUP_MAX) {
+            const int cnt = (int)std::min<size_t>(st::GROUP_MAX, grp[f].size() - c);
+            const st_status r = st::gemm_group(grp[f].data() + c, cnt, (f & 1) != 0, (f & 2) != 0, s);
+            if (r) return r;
+        }
+    for (const int64_t i : rest) {
+        const st_gemm &g = gemms[i];
+        const st_status r = gemm_impl(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n, &g.epi, g.use_f16 != 0, s);
+        if (r) return r;
+    }
+    return ST_OK;
 }
 
 extern "C" st_status st_ndarray_matmul(const float *a, const float *b, float *out, int64_t m, int64_t k,

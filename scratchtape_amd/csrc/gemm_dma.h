@@ -35,4 +35,14 @@ struct DmaGemm {
 // otherwise true, with *status the launch status.
 bool gemm_dma(const DmaGemm &g, hipStream_t stream, st_status *status);
 
+// Grouped launches (gemm_group.hip): at most GROUP_MAX GEMMs of one route
+// (f16 or f32) and one tile shape (group_tall: m % 256 == 0, 256-row tiles;
+// else 128-row tiles) per launch, each of them group_eligible (m % 128 == 0,
+// n % 128 == 0, k % 32 == 0, k >= 128, 16-byte aligned operands, strides and
+// leading dimensions that fit the kernel's 32-bit fields).
+constexpr int GROUP_MAX = 16;
+bool group_eligible(const DmaGemm &g);
+bool group_tall(const DmaGemm &g);
+st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream);
+
 }  // namespace st

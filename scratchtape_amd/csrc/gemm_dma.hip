@@ -5,19 +5,7 @@
 // (v_mfma_f32_16x16x4_f32).  Semantics: gpu_step/matmul.rs:26-299 (MatRef
 // addressing, the epilogue in the reference's order, deterministic split-k).
 //
-// LDS layouts (f32, one 32-deep k-stage per operand; a DMA wave-load writes
-// 64 x 16-byte chunks to consecutive LDS slots, so the layout is chosen on the
-// global-address side):
-//  - KC, an operand whose k is contiguous in memory (A not transposed, B
-//    transposed): [row][8 chunks of 4 k]; chunk c of row r sits in slot
-//    r * 8 + (c ^ ((r >> 1) & 7)).  A fragment (8 k of one row per lane) is two
-//    128-bit reads; the swizzle puts the 16 rows a quarter-wave reads in 16
-//    distinct 16-byte bank groups.
-//  - RC, an operand whose rows are contiguous (A transposed, B not): [k][rows],
-//    line kk holding rows in chunks of 4 rotated by 16 rows per group of 8 k:
-//    chunk q of line kk sits in slot kk * Q + (q + 4 * ((kk >> 3) & 3)) % Q,
-//    Q = ROWS / 4.  A fragment is eight 32-bit reads; the 64 lanes of each read
-//    hit 64 distinct banks.
+// LDS layouts and the DMA / wait / barrier helpers: dma_tile.h.
 //
 // The finished tile goes through LDS once more so that every store (and every
 // epilogue load) moves whole 16-byte runs of a row.  Split-k (few output
@@ -29,15 +17,14 @@
 #include <cstring>
 #include <type_traits>
 
+#include "dma_tile.h"
 #include "gemm_dma.h"
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using namespace dma;
 
 constexpr int THREADS = 256;
-constexpr int BK = 32;  // k per stage
 
 struct KArgs {
     const float *a, *b;
@@ -53,107 +40,6 @@ struct KArgs {
     int32_t has_cs, relu, accumulate;
     int32_t m, n, k, splits, slice_k;
 };
-
-// 16 bytes per lane from global memory to LDS: lane l's 16 bytes from gptr
-// land at LDS byte address lds_addr + 16 l (lds_addr wave-uniform, passed in
-// M0).  Issued as inline assembly so that the compiler sees no LDS store in
-// flight: it would otherwise wait for every DMA before each LDS read (it cannot
-// tell which stage a DMA writes).  Completion is tracked by this file's
-// explicit vmcnt waits, followed by a workgroup barrier, before any wave reads
-// the stage.  M0 is saved and restored around the load, so the compiler's view
-// of it stays valid, and one wait state separates the M0 write from the LDS
-// DMA that reads it (a gfx9 hazard the compiler does not guard in inline asm).
-__device__ __forceinline__ void dma16(const float *gptr, uint32_t lds_addr) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(gptr), "s"(lds_addr)
-        : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr_of(const float *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
-}
-
-// Waits until at most N vector-memory instructions of this wave are in flight.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Waits until this wave's DMA of the oldest stage in flight has landed, with
-// `ahead` (0 .. MAXA) younger stages of L instructions each still in flight.
-template <int L, int MAXA>
-__device__ __forceinline__ void wait_stage(int ahead) {
-    if constexpr (MAXA >= 4) {
-        if (ahead >= 4) return wait_vm<4 * L>();
-    }
-    if constexpr (MAXA >= 3) {
-        if (ahead == 3) return wait_vm<3 * L>();
-    }
-    if constexpr (MAXA >= 2) {
-        if (ahead == 2) return wait_vm<2 * L>();
-    }
-    if constexpr (MAXA >= 1) {
-        if (ahead == 1) return wait_vm<L>();
-    }
-    wait_vm<0>();
-}
-
-// Workgroup barrier without the memory fence of __syncthreads() (which would
-// wait for every load of this wave, the DMA of the younger stages included);
-// the empty asm statements keep the compiler from moving memory accesses
-// across it.
-__device__ __forceinline__ void bar() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Element offset (from the operand's matrix base, at k = 0) of the 16 bytes
-// that DMA slot p of a ROWS x 32 stage tile receives.
-template <int ROWS, bool KC>
-__device__ __forceinline__ int64_t slot_src(int p, int64_t ld, int row0) {
-    if constexpr (KC) {
-        const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
-        return (int64_t)(row0 + r) * ld + 4 * c;
-    } else {
-        constexpr int Q = ROWS / 4;
-        const int kk = p / Q, s = p % Q;
-        const int q = (s - 4 * ((kk >> 3) & 3) + 4 * Q) % Q;
-        return (int64_t)kk * ld + row0 + 4 * q;
-    }
-}
-
-// The 8 values (k = 8g .. 8g + 7 of the stage) of row r of a stage tile.
-template <int ROWS, bool KC>
-__device__ __forceinline__ void frag(const float *t, int r, int g, float (&x)[8]) {
-    if constexpr (KC) {
-        const int sw = (r >> 1) & 7;
-        const f32x4 lo = *reinterpret_cast<const f32x4 *>(t + (r * 8 + ((2 * g) ^ sw)) * 4);
-        const f32x4 hi = *reinterpret_cast<const f32x4 *>(t + (r * 8 + ((2 * g + 1) ^ sw)) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            x[e] = lo[e];
-            x[4 + e] = hi[e];
-        }
-    } else {
-        constexpr int Q = ROWS / 4;
-        const int q = ((r >> 2) + 4 * g) % Q;  // (kk >> 3) & 3 == g for kk = 8g + u
-#pragma unroll
-        for (int u = 0; u < 8; u++) x[u] = t[((8 * g + u) * Q + q) * 4 + (r & 3)];
-    }
-}
-
-__device__ __forceinline__ int64_t zoff(int64_t z, int64_t group, int64_t stride, int64_t inner) {
-    return (z / group) * stride + (z % group) * inner;
-}
 
 // NS k-stages resident in LDS, NS - 1 of them in flight while one is multiplied.
 template <int BM, int BN, int NS, bool TA, bool TB, bool F16>

@@ -1,0 +1,540 @@
+// Grouped GEMM: several independent GEMMs (no one reads or writes what
+// another writes) in one persistent launch of the LDS-DMA tile engine
+// (dma_tile.h).  The reference issues such GEMMs back to back on its queue,
+// e.g. the dW and dx of a Linear backward (gpu_step/tape.rs:324-347); each
+// launch of its own pays the launch, the ramp of the first k-stages and the
+// drain of the last tile, which at the d_model-256 step shapes (0.5-2 GFLOP
+// per GEMM) cost as much as the arithmetic.  Here every output tile (256 x 128,
+// or 128 x 128 for GEMMs whose m is not a multiple of 256) or split-k slice of
+// every GEMM of the group is a unit of work; one workgroup per CU walks its
+// units and starts the DMA of the next unit's first k-stages while it
+// multiplies the last stages of the current one, so the ring of stages never
+// drains between tiles.
+//
+// Units are dealt to the 8 XCDs (a workgroup's XCD is its id mod 8) as one
+// contiguous block of each GEMM's tiles per XCD, so the tiles an XCD runs
+// together share operand panels in its L2; GEMMs are ordered by k-stages per
+// unit, longest first, and each XCD's workgroups take its units round-robin.
+//
+// Per element the arithmetic is that of gemm_dma.hip (the same k-stage order
+// and matrix-core instructions), so a GEMM that is not split here gives the
+// bits of the single-GEMM kernel when that one does not split either.  Split-k
+// (free epilogue but +=, packed out) writes per-slice partials that
+// k_sum_group adds in ascending slice order with accumulate and the column
+// sums, as k_sum_slices does (matmul.rs:259-299).
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "dma_tile.h"
+#include "gemm_dma.h"
+
+namespace {
+
+using namespace dma;
+
+constexpr int XCDS = 8;
+constexpr int TN = 128;  // output tile columns (both shapes)
+
+// Tile shapes: TM x 128 output tiles, WGM x 2 waves of 64 x 64 each, NS
+// k-stages of 32 resident in LDS.  256-row tiles (8 waves, 144 KB) read 25 %
+// fewer operand bytes per flop and keep two waves per SIMD, so one wave's
+// LDS reads and conversions overlap the other's matrix-core work; 128-row
+// tiles (4 waves, 128 KB) serve GEMMs whose m is not a multiple of 256.
+template <int TM_, int WGM_, int NS_>
+struct Cfg {
+    static constexpr int TM = TM_, WGM = WGM_, WGN = 2, NS = NS_;
+    static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+    static constexpr int WM = TM / WGM, WN = TN / WGN, FM = WM / 16, FN = WN / 16;
+    static constexpr int SA = TM * BK, SB = TN * BK;           // floats per stage
+    static constexpr int LA = TM / (8 * WAVES), LB = TN / (8 * WAVES);  // DMA wave-loads per wave per stage
+    static_assert(WM == 64 && WN == 64, "64 x 64 per wave");
+    static_assert(NS * (SA + SB) * 4 <= 160 * 1024, "LDS");
+};
+using Tall = Cfg<256, 4, 3>;
+using Square = Cfg<128, 2, 4>;
+
+enum { F_TA = 1, F_TB = 2, F_RELU = 4, F_ACC = 8, F_CS = 16 };
+
+struct GProb {
+    const float *a, *b;
+    float *out;  // the output, or this GEMM's split partials [batch][splits][m][n]
+    const float *bias, *mask, *res;
+    float *cs;  // column-sum destination (out buffer + col_sum_off), or the split partials [batch][splits][n]
+    int64_t a_stride, a_inner, b_stride, b_inner, o_stride, o_inner, bias_stride, cs_stride;
+    int32_t a_group, b_group, o_group;
+    int32_t lda, ldb, ldo;
+    int32_t m, n, k, splits, slice_k;
+    int32_t flags;
+    int32_t tiles_n, tiles_m;
+    int32_t units;  // tiles_n * tiles_m * batch * splits
+    int32_t pad;
+};
+
+struct GroupArgs {
+    GProb p[st::GROUP_MAX];
+    int32_t count;
+};
+static_assert(sizeof(GroupArgs) <= 4000, "kernel arguments");
+
+// A unit of work of one workgroup: one output tile (or split slice) of one GEMM.
+template <class C>
+struct Unit {
+    int32_t p;  // GEMM index, -1: none
+    int32_t nst, row0, col0, slice;
+    int64_t zb;
+    bool akc, bkc;
+    const float *abase, *bbase;
+    int64_t aoff[C::LA], boff[C::LB];
+    int64_t astep, bstep;
+};
+
+template <int ROWS>
+__device__ __forceinline__ int64_t slot_src_rt(bool kc, int p, int64_t ld, int row0) {
+    return kc ? slot_src<ROWS, true>(p, ld, row0) : slot_src<ROWS, false>(p, ld, row0);
+}
+
+// Unit j of XCD x's list (every GEMM's block of tiles for XCD x, in order).
+template <class C>
+__device__ void locate(const GroupArgs &ga, int x, int j, int wave, int lane, Unit<C> &u) {
+    u.p = -1;
+    int t = 0;
+    for (int p = 0; p < ga.count; p++) {
+        const int U = ga.p[p].units;
+        const int s0 = (int)((int64_t)x * U / XCDS), s1 = (int)((int64_t)(x + 1) * U / XCDS);
+        if (j < s1 - s0) {
+            u.p = p;
+            t = s0 + j;
+            break;
+        }
+        j -= s1 - s0;
+    }
+    if (u.p < 0) return;
+    const GProb &g = ga.p[u.p];
+    const int bx = t % g.tiles_n;
+    const int r = t / g.tiles_n;
+    const int by = r % g.tiles_m;
+    const int zs = r / g.tiles_m;
+    u.zb = zs / g.splits;
+    u.slice = zs % g.splits;
+    u.row0 = by * C::TM;
+    u.col0 = bx * TN;
+    const int kbeg = u.slice * g.slice_k;
+    u.nst = (min(g.k, kbeg + g.slice_k) - kbeg) / BK;
+    u.akc = !(g.flags & F_TA);
+    u.bkc = (g.flags & F_TB) != 0;
+    u.abase = g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner);
+    u.bbase = g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner);
+#pragma unroll
+    for (int i = 0; i < C::LA; i++)
+        u.aoff[i] = slot_src_rt<C::TM>(u.akc, (wave * C::LA + i) * 64 + lane, g.lda, u.row0) +
+                    (u.akc ? kbeg : (int64_t)kbeg * g.lda);
+#pragma unroll
+    for (int i = 0; i < C::LB; i++)
+        u.boff[i] = slot_src_rt<TN>(u.bkc, (wave * C::LB + i) * 64 + lane, g.ldb, u.col0) +
+                    (u.bkc ? kbeg : (int64_t)kbeg * g.ldb);
+    u.astep = u.akc ? BK : (int64_t)BK * g.lda;
+    u.bstep = u.bkc ? BK : (int64_t)BK * g.ldb;
+}
+
+// grid: a multiple of 8 workgroups, at most one per CU (the ring takes most
+// of the LDS).  Every GEMM's unit has at least NS - 1 k-stages.
+template <class C, bool F16>
+__global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
+    constexpr int TM = C::TM, NS = C::NS, SA = C::SA, SB = C::SB, LA = C::LA, LB = C::LB;
+    constexpr int WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
+    __shared__ __attribute__((aligned(16))) float lds[NS * (SA + SB)];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::WGN, wn = wave % C::WGN;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int x = blockIdx.x % XCDS, L = gridDim.x / XCDS;
+    int j = blockIdx.x / XCDS;
+
+    Unit<C> cur, nxt;
+    locate(ga, x, j, wave, lane, cur);
+    if (cur.p < 0) return;
+    locate(ga, x, j + L, wave, lane, nxt);
+
+    auto issue = [&](const Unit<C> &u, int st, int vst) {
+        const uint32_t base = lds_addr_of(lds + (vst % NS) * (SA + SB));
+#pragma unroll
+        for (int i = 0; i < LA; i++) dma16(u.abase + u.aoff[i] + st * u.astep, base + (wave_u * LA + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < LB; i++)
+            dma16(u.bbase + u.boff[i] + st * u.bstep, base + SA * 4 + (wave_u * LB + i) * 1024);
+    };
+
+    int vb = 0;  // ring position (virtual stage number) of cur's stage 0
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) issue(cur, st, st);
+
+    f32x4 acc[FM][FN];
+    while (true) {
+        const GProb &g = ga.p[cur.p];
+        const bool do_cs = (g.flags & F_CS) && cur.row0 == 0;
+        float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < TN), this slice
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // Stage st of cur: wait for this wave's DMA of it (younger stages,
+        // possibly the next unit's, stay in flight), barrier (every wave's
+        // part landed, every wave done with the previous stage), start the
+        // stage NS - 1 ahead (of cur, or of nxt once cur's run out) into the
+        // slot just freed, multiply.
+        auto kloop = [&](auto akc_c, auto bkc_c) {
+            constexpr bool AKC = decltype(akc_c)::value, BKC = decltype(bkc_c)::value;
+            const int nst = cur.nst;
+            const bool more = nxt.p >= 0;
+            for (int st = 0; st < nst; st++) {
+                const int issued = more ? st + NS - 1 : min(st + NS - 1, nst);
+                wait_stage<LA + LB, NS - 2>(issued - st - 1);
+                bar();
+                const int is = st + NS - 1;
+                if (is < nst)
+                    issue(cur, is, vb + is);
+                else if (more)
+                    issue(nxt, is - nst, vb + is);
+                const float *la = lds + ((vb + st) % NS) * (SA + SB);
+                const float *lb = la + SA;
+                const int gq = lane >> 4;
+                if constexpr (F16) {
+                    half8 af[FM], bf[FN];
+#pragma unroll
+                    for (int i = 0; i < FM; i++) {
+                        float v[8];
+                        frag<TM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, v);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) af[i][e] = (_Float16)v[e];
+                    }
+#pragma unroll
+                    for (int jn = 0; jn < FN; jn++) {
+                        float v[8];
+                        frag<TN, BKC>(lb, wn * WN + jn * 16 + (lane & 15), gq, v);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) bf[jn][e] = (_Float16)v[e];
+                    }
+#pragma unroll
+                    for (int i = 0; i < FM; i++)
+#pragma unroll
+                        for (int jn = 0; jn < FN; jn++)
+                            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+                } else {
+                    float ax[FM][8], bx8[FN][8];
+#pragma unroll
+                    for (int i = 0; i < FM; i++) frag<TM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, ax[i]);
+#pragma unroll
+                    for (int jn = 0; jn < FN; jn++) frag<TN, BKC>(lb, wn * WN + jn * 16 + (lane & 15), gq, bx8[jn]);
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+#pragma unroll
+                        for (int i = 0; i < FM; i++)
+#pragma unroll
+                            for (int jn = 0; jn < FN; jn++)
+                                acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[i][u], bx8[jn][u], acc[i][jn], 0,
+                                                                                   0, 0);
+                }
+                if (do_cs && tid < TN) {
+                    float v[8];
+#pragma unroll
+                    for (int gg = 0; gg < 4; gg++) {
+                        frag<TN, BKC>(lb, tid, gg, v);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) cs_acc += v[e];
+                    }
+                }
+            }
+        };
+        if (cur.akc) {
+            if (cur.bkc)
+                kloop(std::true_type(), std::true_type());
+            else
+                kloop(std::true_type(), std::false_type());
+        } else {
+            if (cur.bkc)
+                kloop(std::false_type(), std::true_type());
+            else
+                kloop(std::false_type(), std::false_type());
+        }
+
+        // Epilogue straight from the accumulators (lane l holds rows
+        // 4 (l / 16) .. + 3 of column l % 16 of each 16 x 16 block: 16 lanes
+        // store 64 consecutive bytes of a row), in the reference's order:
+        // + bias, ReLU, zero where mask <= 0, + residual, + out.
+        if (do_cs && tid < TN) {
+            if (g.splits > 1)
+                g.cs[(cur.zb * g.splits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
+            else
+                g.cs[cur.zb * g.cs_stride + cur.col0 + tid] += cs_acc;
+        }
+        const int rbase = cur.row0 + wm * WM + 4 * (lane >> 4);
+        const int cbase = cur.col0 + wn * WN + (lane & 15);
+        if (g.splits > 1) {
+            float *P = g.out + (cur.zb * g.splits + cur.slice) * (int64_t)g.m * g.n;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int jn = 0; jn < FN; jn++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        P[(int64_t)(rbase + i * 16 + r) * g.n + cbase + jn * 16] = acc[i][jn][r];
+        } else {
+            const int64_t o0 = zoff(cur.zb, g.o_group, g.o_stride, g.o_inner);
+            float bv[FN];
+#pragma unroll
+            for (int jn = 0; jn < FN; jn++) bv[jn] = g.bias ? g.bias[cur.zb * g.bias_stride + cbase + jn * 16] : 0.f;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int jn = 0; jn < FN; jn++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int64_t idx = o0 + (int64_t)(rbase + i * 16 + r) * g.ldo + cbase + jn * 16;
+                        float v = acc[i][jn][r];
+                        if (g.bias) v += bv[jn];
+                        if ((g.flags & F_RELU) && v < 0.f) v = 0.f;
+                        if (g.mask && g.mask[idx] <= 0.f) v = 0.f;
+                        if (g.res) v += g.res[idx];
+                        if (g.flags & F_ACC) v += g.out[idx];
+                        g.out[idx] = v;
+                    }
+        }
+
+        vb += cur.nst;
+        if (nxt.p < 0) break;
+        cur = nxt;
+        j += L;
+        locate(ga, x, j + L, wave, lane, nxt);
+    }
+}
+
+struct SProb {
+    const float *part;
+    float *out;
+    const float *cs_part;
+    float *cs_dst;
+    int64_t mn4, o_stride, cs_stride, n, batch, t0;
+    int32_t splits, accumulate;
+};
+
+struct SumArgs {
+    SProb p[st::GROUP_MAX];
+    int32_t count;
+};
+
+// The split GEMMs' partial sums, one thread per 4 outputs (then one per
+// column sum), as k_sum_slices; thread ranges per GEMM start at t0.
+__global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int p = 0;
+    while (p + 1 < sa.count && e >= sa.p[p + 1].t0) p++;
+    const SProb &s = sa.p[p];
+    const int64_t local = e - s.t0;
+    if (local < 0) return;
+    if (local < s.batch * s.mn4) {
+        const int64_t b = local / s.mn4, i = local % s.mn4;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(s.part) + b * s.splits * s.mn4 + i;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int sl = 0; sl < s.splits; sl++) v += src[sl * s.mn4];
+        f32x4 *o = reinterpret_cast<f32x4 *>(s.out + b * s.o_stride) + i;
+        if (s.accumulate) v += *o;
+        *o = v;
+    } else if (s.cs_part) {
+        const int64_t c = local - s.batch * s.mn4;
+        if (c < s.batch * s.n) {
+            const int64_t b = c / s.n, jn = c % s.n;
+            float v = 0.f;
+            for (int sl = 0; sl < s.splits; sl++) v += s.cs_part[(b * s.splits + sl) * s.n + jn];
+            s.cs_dst[b * s.cs_stride + jn] += v;
+        }
+    }
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool fits32(int64_t v) { return v >= 0 && v <= INT32_MAX; }
+
+bool can_split(const st::DmaGemm &d) {
+    return !d.bias && !d.relu && !d.mask && !d.res && d.ldo == d.n && d.o_group == 1 &&
+           (d.batch == 1 || d.o_stride == d.m * d.n);
+}
+
+int cu_count() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+}  // namespace
+
+namespace st {
+
+bool group_eligible(const DmaGemm &d) {
+    if (d.m % Square::TM || d.n % TN || d.k % BK || d.k < 4 * BK) return false;
+    if (!al16(d.a) || !al16(d.b) || !al16(d.out) || (d.mask && !al16(d.mask)) || (d.res && !al16(d.res)))
+        return false;
+    if (d.lda % 4 || d.ldb % 4 || d.a_stride % 4 || d.a_inner % 4 || d.b_stride % 4 || d.b_inner % 4) return false;
+    if (!fits32(d.lda) || !fits32(d.ldb) || !fits32(d.ldo) || !fits32(d.a_group) || !fits32(d.b_group) ||
+        !fits32(d.o_group))
+        return false;
+    return fits32(d.batch * (d.m / Square::TM) * (d.n / TN) * (d.k / BK));
+}
+
+bool group_tall(const DmaGemm &d) { return d.m % Tall::TM == 0; }
+
+}  // namespace st
+
+namespace {
+
+template <class C>
+st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_t stream) {
+    using st::DmaGemm;
+    using st::fail;
+    constexpr int TM = C::TM, NS = C::NS;
+    if (count <= 0) return ST_OK;
+    if (count > st::GROUP_MAX) return fail(ST_ERR_INVALID, "at most %d GEMMs per grouped launch", st::GROUP_MAX);
+    static thread_local int cus_cached = 0;
+    if (!cus_cached) cus_cached = cu_count();
+    const int cus = cus_cached;
+
+    // Split-k where the epilogue allows it, so that no unit holds more
+    // k-stages than a CU's fair share of the whole group (nor fewer than 4).
+    std::vector<int64_t> splits(count, 1), slice_k(count, 0);
+    double total = 0;
+    for (int i = 0; i < count; i++)
+        total += (double)items[i].batch * (items[i].m / TM) * (items[i].n / TN) * (items[i].k / BK);
+    const double fair = std::max(8.0, total / cus);
+    for (int i = 0; i < count; i++) {
+        const DmaGemm &d = items[i];
+        int64_t sp = 1;
+        if (can_split(d))
+            while ((double)d.k / BK / sp > fair && d.k / (2 * sp) >= 4 * BK) sp *= 2;
+        int64_t sk = cdiv(cdiv(d.k, sp), BK) * BK;
+        int64_t n_sp = cdiv(d.k, sk);
+        // Every slice keeps at least NS - 1 stages.
+        while (n_sp > 1 && d.k - (n_sp - 1) * sk < (NS - 1) * BK) {
+            sp /= 2;
+            sk = cdiv(cdiv(d.k, sp), BK) * BK;
+            n_sp = cdiv(d.k, sk);
+        }
+        splits[i] = n_sp;
+        slice_k[i] = sk;
+    }
+    // Longest units first.
+    std::vector<int> order(count);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return slice_k[x] > slice_k[y]; });
+
+    size_t part_floats = 0;
+    std::vector<size_t> part_off(count, 0), cs_off(count, 0);
+    for (int i = 0; i < count; i++) {
+        if (splits[i] == 1) continue;
+        const DmaGemm &d = items[i];
+        part_off[i] = part_floats;
+        part_floats += (size_t)(d.batch * splits[i] * d.m * d.n);
+        cs_off[i] = part_floats;
+        if (d.has_cs) part_floats += (size_t)(d.batch * splits[i] * d.n);
+    }
+    float *part = nullptr;
+    if (part_floats) {
+        part = static_cast<float *>(st::scratch(st::SCRATCH_SPLITK, part_floats * sizeof(float)));
+        if (!part) return ST_ERR_OOM;
+    }
+
+    GroupArgs ga;
+    std::memset(&ga, 0, sizeof ga);
+    SumArgs sa;
+    std::memset(&sa, 0, sizeof sa);
+    int64_t units = 0, sum_threads = 0;
+    ga.count = count;
+    for (int o = 0; o < count; o++) {
+        const int i = order[o];
+        const DmaGemm &d = items[i];
+        GProb &g = ga.p[o];
+        g.a = d.a;
+        g.b = d.b;
+        g.a_stride = d.a_stride;
+        g.a_inner = d.a_inner;
+        g.a_group = (int32_t)d.a_group;
+        g.lda = (int32_t)d.lda;
+        g.b_stride = d.b_stride;
+        g.b_inner = d.b_inner;
+        g.b_group = (int32_t)d.b_group;
+        g.ldb = (int32_t)d.ldb;
+        g.m = (int32_t)d.m;
+        g.n = (int32_t)d.n;
+        g.k = (int32_t)d.k;
+        g.splits = (int32_t)splits[i];
+        g.slice_k = (int32_t)slice_k[i];
+        g.flags = (d.ta ? F_TA : 0) | (d.tb ? F_TB : 0) | (d.relu ? F_RELU : 0) | (d.accumulate ? F_ACC : 0) |
+                  (d.has_cs ? F_CS : 0);
+        g.tiles_n = (int32_t)(d.n / TN);
+        g.tiles_m = (int32_t)(d.m / TM);
+        const int64_t u = d.batch * g.tiles_n * g.tiles_m * splits[i];
+        if (!fits32(u) || !fits32(units + u)) return fail(ST_ERR_INVALID, "grouped GEMM: too many tiles");
+        g.units = (int32_t)u;
+        units += u;
+        if (splits[i] > 1) {
+            // No epilogue but += and column sums, both applied by k_sum_group.
+            g.out = part + part_off[i];
+            g.o_stride = d.m * d.n;
+            g.o_group = 1;
+            g.ldo = (int32_t)d.n;
+            g.cs = part + cs_off[i];
+            g.cs_stride = d.n;
+            g.flags &= ~F_ACC;
+            SProb &s = sa.p[sa.count++];
+            s.part = g.out;
+            s.out = d.out;
+            s.cs_part = d.has_cs ? g.cs : nullptr;
+            s.cs_dst = d.cs;
+            s.mn4 = d.m * d.n / 4;
+            s.o_stride = d.o_stride;
+            s.cs_stride = d.cs_stride;
+            s.n = d.n;
+            s.batch = d.batch;
+            s.t0 = sum_threads;
+            s.splits = (int32_t)splits[i];
+            s.accumulate = d.accumulate;
+            sum_threads += d.batch * s.mn4 + (d.has_cs ? d.batch * d.n : 0);
+        } else {
+            g.out = d.out;
+            g.o_stride = d.o_stride;
+            g.o_inner = d.o_inner;
+            g.o_group = (int32_t)d.o_group;
+            g.ldo = (int32_t)d.ldo;
+            g.bias = d.bias;
+            g.bias_stride = d.bias_stride;
+            g.mask = d.mask;
+            g.res = d.res;
+            g.cs = d.cs;
+            g.cs_stride = d.cs_stride;
+        }
+    }
+    const int64_t wgs = std::min<int64_t>(cus / XCDS * XCDS, cdiv(units, XCDS) * XCDS);
+    void (*kern)(GroupArgs) = f16 ? &k_gemm_group<C, true> : &k_gemm_group<C, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)std::max<int64_t>(XCDS, wgs)), dim3(C::THREADS), 0, stream, ga);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && sa.count) {
+        hipLaunchKernelGGL(k_sum_group, dim3((unsigned)cdiv(sum_threads, 256)), dim3(256), 0, stream, sa);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? ST_OK : fail(ST_ERR_HIP, "grouped GEMM launch failed: %s", hipGetErrorString(e));
+}
+
+}  // namespace
+
+namespace st {
+
+st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream) {
+    return tall ? launch_group<Tall>(items, count, f16, stream) : launch_group<Square>(items, count, f16, stream);
+}
+
+}  // namespace st

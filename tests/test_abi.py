@@ -44,6 +44,9 @@ def test_struct_layouts_match_the_header():
     # st_matref: p, off, stride, trans, reserved, ld, group, inner
     assert _lib.StMatRef.inner.offset == 48 and _lib.ctypes.sizeof(_lib.StMatRef) == 56
     assert _lib.StEpilogue.col_sum_stride.offset == 80 and _lib.ctypes.sizeof(_lib.StEpilogue) == 88
+    # st_gemm: a, b, out (st_matref), epi, batch, m, k, n, use_f16, reserved
+    assert _lib.StGemm.epi.offset == 168 and _lib.StGemm.batch.offset == 256
+    assert _lib.StGemm.use_f16.offset == 288 and _lib.ctypes.sizeof(_lib.StGemm) == 296
 
 
 def test_null_arguments_are_rejected_without_a_device():
@@ -53,6 +56,12 @@ def test_null_arguments_are_rejected_without_a_device():
     assert b"NULL" in L.st_last_error()
     rc = L.st_softmax(None, None, 4, 4, 4, 1.0, 1, 0, None)
     assert rc == _lib.ST_ERR_INVALID
+    rc = L.st_matmul_grouped(None, 2, None)
+    assert rc == _lib.ST_ERR_INVALID
+    g = (_lib.StGemm * 2)()
+    g[1].batch, g[1].m, g[1].k, g[1].n = 1, 4, 4, 4   # g[1].a.p is NULL
+    rc = L.st_matmul_grouped(g, 2, None)
+    assert rc == _lib.ST_ERR_INVALID and b"GEMM 0 of the group" in L.st_last_error()
 
 
 def test_ndarray_matmul_shape_asserts_like_the_reference():

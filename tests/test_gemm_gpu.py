@@ -69,9 +69,10 @@ def rel_err(got, want):
     return float(np.max(np.abs(got - want))) / max(scale, 1e-30)
 
 
-def run_case(dev, ci, case, use_f16, aligned16=False, packed=False):
-    """aligned16: every operand, stride and epilogue tensor on 16-byte boundaries (the layouts the
-    LDS-DMA kernel takes); packed: out matrices back to back (the layout split-k needs)."""
+def prep_case(dev, ci, case, use_f16, aligned16=False, packed=False):
+    """Buffers, the matmul_with arguments and the oracle's answers for one case.
+    aligned16: every operand, stride and epilogue tensor on 16-byte boundaries (the layouts the
+    LDS-DMA kernels take); packed: out matrices back to back (the layout split-k needs)."""
     batch, m, k, n, ta, tb, has_bias, relu, has_mask, has_res, acc = case
     rng = oracle.Rng(5 + ci)
     gauss = rng.gaussian
@@ -104,18 +105,29 @@ def run_case(dev, ci, case, use_f16, aligned16=False, packed=False):
     epi = Epilogue(bias=(biash, bias_off) if has_bias else None, bias_stride=bias_stride, relu=relu,
                    mask=(maskh, m_off) if has_mask else None, residual=(resh, r_off) if has_res else None,
                    accumulate=acc, col_sum=(cs_off, cs_stride))
-    st.matmul_with(MatRef(ah, off=a_off, stride=sa, trans=ta), MatRef(bh, off=b_off, stride=sb, trans=tb),
-                   MatRef(oh, off=o_off, stride=so), batch, m, k, n, epi, use_f16)
-    got = oh.cpu().numpy()
-    what = f"case {ci} {case} f16_route={f16}"
-    body, cs = slice(0, cs_off), slice(cs_off, None)
-    if f16:
-        assert rel_err(got[body], want16[body]) <= 1e-5, what
-        assert rel_err(got[body], want32[body]) <= 2e-3, what
-        assert rel_err(got[cs], want32[cs]) <= 1e-3, what
+    call = (MatRef(ah, off=a_off, stride=sa, trans=ta), MatRef(bh, off=b_off, stride=sb, trans=tb),
+            MatRef(oh, off=o_off, stride=so), batch, m, k, n, epi, use_f16)
+    return dict(call=call, oh=oh, out0=out0, want16=want16, want32=want32, cs_off=cs_off, f16=f16,
+                what=f"case {ci} {case} f16_route={f16}")
+
+
+def check_case(p, got=None):
+    got = p["oh"].cpu().numpy() if got is None else got
+    body, cs = slice(0, p["cs_off"]), slice(p["cs_off"], None)
+    what = p["what"]
+    if p["f16"]:
+        assert rel_err(got[body], p["want16"][body]) <= 1e-5, what
+        assert rel_err(got[body], p["want32"][body]) <= 2e-3, what
+        assert rel_err(got[cs], p["want32"][cs]) <= 1e-3, what
     else:
-        assert rel_err(got[body], want32[body]) <= 1e-5, what
-        assert rel_err(got[cs], want32[cs]) <= 1e-4, what
+        assert rel_err(got[body], p["want32"][body]) <= 1e-5, what
+        assert rel_err(got[cs], p["want32"][cs]) <= 1e-4, what
+
+
+def run_case(dev, ci, case, use_f16, aligned16=False, packed=False):
+    p = prep_case(dev, ci, case, use_f16, aligned16, packed)
+    st.matmul_with(*p["call"])
+    check_case(p)
 
 
 # Shapes for the LDS-DMA kernel (m, n tile-divisible, k % 32 == 0), run with 16-byte aligned
@@ -269,3 +281,105 @@ def test_bad_arguments_raise_with_the_reference_message(dev):
     x = torch.zeros(16, device=dev)
     with pytest.raises(st.ScratchtapeError, match="out is stored row-major"):
         st.matmul(MatRef(x), MatRef(x), MatRef(x, trans=True), 1, 4, 4, 4)
+
+
+# Grouped launches (st_matmul_grouped): GEMMs that tile by 128 x 128 share one
+# persistent launch per route; the others (last two) run one by one.
+# (batch, m, k, n, trans_a, trans_b, bias, relu, mask, residual, accumulate, packed)
+GROUP_CASES = [
+    (1, 256, 256, 384, False, False, True, True, False, False, False, False),
+    (1, 128, 1024, 256, True, False, False, False, False, False, True, True),
+    (2, 128, 128, 128, False, True, False, False, True, True, False, False),
+    (1, 384, 512, 128, True, True, True, False, False, False, False, False),
+    (3, 128, 256, 128, True, False, False, False, False, False, True, True),
+    (1, 128, 128, 256, False, False, False, False, False, False, True, False),
+    (1, 256, 4096, 128, True, False, False, False, False, False, False, True),
+    (1, 64, 64, 64, False, False, True, False, False, False, False, False),
+    (1, 70, 35, 20, True, False, False, False, False, True, False, False),
+]
+
+
+def group_preps(dev, use_f16, idx):
+    out = []
+    for i in idx:
+        c = GROUP_CASES[i]
+        out.append(prep_case(dev, 200 + i, c[:11], use_f16, aligned16=True, packed=c[11]))
+    return out
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+def test_grouped_matches_oracle(dev, use_f16):
+    ps = group_preps(dev, use_f16, range(len(GROUP_CASES)))
+    st.matmul_grouped([p["call"] for p in ps])
+    for p in ps:
+        check_case(p)
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+def test_grouped_with_256_row_tiles_matches_oracle(dev, use_f16):
+    # A 4096 x 2048 GEMM gives the route 256 tiles of 256 rows, so every GEMM of the
+    # group whose m is a multiple of 256 (cases 0 and 6) runs on the 8-wave 256-row
+    # kernel, the others on the 128-row one.
+    ps = group_preps(dev, use_f16, range(len(GROUP_CASES)))
+    ps.append(prep_case(dev, 300, (1, 4096, 128, 2048, False, False, True, False, False, False, True), use_f16,
+                        aligned16=True))
+    st.matmul_grouped([p["call"] for p in ps])
+    for p in ps:
+        check_case(p)
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+def test_grouped_of_one_and_repeated(dev, use_f16):
+    # A group of one (split-k over many slices: the only GEMM of the launch), then
+    # the same group again: the second call starts from the first call's output.
+    ps = group_preps(dev, use_f16, [6])
+    st.matmul_grouped([ps[0]["call"]])
+    check_case(ps[0])
+    ps = group_preps(dev, use_f16, [1, 4])
+    for _ in range(2):
+        st.matmul_grouped([p["call"] for p in ps])
+    for p in ps:
+        # accumulate: out = out0 + 2 * product (and column sums twice); the route's
+        # product is the f16-rounded one on the f16 route, column sums are f32
+        prod = p["want32"] - p["out0"]
+        if p["f16"]:
+            body = slice(0, p["cs_off"])
+            prod[body] = p["want16"][body] - p["out0"][body]
+        check_case(p, got=p["oh"].cpu().numpy() - prod)
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+def test_grouped_equals_single_calls_bit_for_bit_without_split(dev, use_f16):
+    # GEMMs with a bias, mask or residual never split: each output element is
+    # the same sequence of operations in the grouped and the single-GEMM kernel.
+    idx = [0, 2, 3]
+    ps = group_preps(dev, use_f16, idx)
+    st.matmul_grouped([p["call"] for p in ps])
+    got = [p["oh"].cpu().numpy() for p in ps]
+    for p, g in zip(ps, got):
+        p["oh"].copy_(torch.from_numpy(p["out0"]).to(dev))
+        st.matmul_with(*p["call"])
+        np.testing.assert_array_equal(g, p["oh"].cpu().numpy(), err_msg=p["what"])
+
+
+@pytest.mark.parametrize("use_f16", [False, True])
+def test_grouped_step_set_matches_torch(dev, use_f16):
+    """The 15 GEMMs of a d_model-256 step (T = 4096) as one group, against torch f32
+    matmuls on the same device (f16 route: 2e-3, f32: 1e-5, scale-relative)."""
+    T, calls, checks = 4096, [], []
+    g = torch.Generator(device="cpu").manual_seed(3)
+    for K, N in [(256, 768), (256, 256), (256, 1024), (1024, 256), (256, 256)]:
+        X, W, dY = (torch.randn(s, generator=g).to(dev) for s in ((T, K), (K, N), (T, N)))
+        W *= 0.02
+        Y, dX, dW = torch.zeros(T, N, device=dev), torch.zeros(T, K, device=dev), torch.zeros(K, N, device=dev)
+        calls += [(MatRef(X), MatRef(W), MatRef(Y), 1, T, K, N, None, use_f16),
+                  (MatRef(dY), MatRef(W, trans=True), MatRef(dX), 1, T, N, K, None, use_f16),
+                  (MatRef(X, trans=True), MatRef(dY), MatRef(dW), 1, K, T, N, None, use_f16)]
+        checks += [(Y, X, W), (dX, dY, W.t()), (dW, X.t(), dY)]
+    st.matmul_grouped(calls)
+    for i, (out, a, b) in enumerate(checks):
+        if use_f16:
+            a, b = a.half().float(), b.half().float()
+        want = (a.contiguous().double() @ b.contiguous().double()).float()
+        err = ((out - want).abs().max() / want.abs().max()).item()
+        assert err <= (2e-3 if use_f16 else 1e-5), (i, err)
