@@ -260,47 +260,63 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                 kloop(std::false_type(), std::false_type());
         }
 
-        // Epilogue straight from the accumulators (lane l holds rows
-        // 4 (l / 16) .. + 3 of column l % 16 of each 16 x 16 block: 16 lanes
-        // store 64 consecutive bytes of a row), in the reference's order:
-        // + bias, ReLU, zero where mask <= 0, + residual, + out.
         if (do_cs && tid < TN) {
             if (g.splits > 1)
                 g.cs[(cur.zb * g.splits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
             else
                 g.cs[cur.zb * g.cs_stride + cur.col0 + tid] += cs_acc;
         }
-        const int rbase = cur.row0 + wm * WM + 4 * (lane >> 4);
-        const int cbase = cur.col0 + wn * WN + (lane & 15);
-        if (g.splits > 1) {
-            float *P = g.out + (cur.zb * g.splits + cur.slice) * (int64_t)g.m * g.n;
+        // Epilogue through LDS: the slot of the unit's last stage is free
+        // until the next unit's first barrier (the next stage issued into it
+        // follows that barrier); once every wave is done reading it, each
+        // wave turns its 64 x 64 accumulators into 16-byte runs of rows, 16
+        // rows at a time (pitch EP: the 16 lanes of a row write 16 consecutive
+        // words and its 4 row groups land 16 banks apart), and stores them
+        // with the epilogue in the reference's order: + bias, ReLU, zero where
+        // mask <= 0, + residual, + out.
+        bar();
+        {
+            constexpr int EP = WN + 4;
+            float *ep = lds + ((vb + cur.nst - 1) % NS) * (SA + SB) + wave * 16 * EP;
+            const bool split = g.splits > 1;
+            float *const P = split ? g.out + (cur.zb * g.splits + cur.slice) * (int64_t)g.m * g.n : nullptr;
+            const int64_t o0 = split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner);
+            const int64_t ld = split ? g.n : g.ldo;
+            float *const obase = split ? P : g.out + o0;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+            for (int i = 0; i < FM; i++) {
 #pragma unroll
                 for (int jn = 0; jn < FN; jn++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        P[(int64_t)(rbase + i * 16 + r) * g.n + cbase + jn * 16] = acc[i][jn][r];
-        } else {
-            const int64_t o0 = zoff(cur.zb, g.o_group, g.o_stride, g.o_inner);
-            float bv[FN];
+                    for (int r = 0; r < 4; r++) ep[(4 * (lane >> 4) + r) * EP + jn * 16 + (lane & 15)] = acc[i][jn][r];
 #pragma unroll
-            for (int jn = 0; jn < FN; jn++) bv[jn] = g.bias ? g.bias[cur.zb * g.bias_stride + cbase + jn * 16] : 0.f;
+                for (int q = 0; q < 16 * WN / 4 / 64; q++) {
+                    const int e = q * 64 + lane, row = e / (WN / 4), c4 = (e % (WN / 4)) * 4;
+                    f32x4 v = *reinterpret_cast<const f32x4 *>(ep + row * EP + c4);
+                    const int grow = cur.row0 + wm * WM + i * 16 + row, gcol = cur.col0 + wn * WN + c4;
+                    const int64_t idx = (int64_t)grow * ld + gcol;
+                    if (!split) {
+                        if (g.bias) {
+                            const float *bp = g.bias + cur.zb * g.bias_stride + gcol;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                            for (int x = 0; x < 4; x++) v[x] += bp[x];
+                        }
+                        if (g.flags & F_RELU) {
 #pragma unroll
-                for (int jn = 0; jn < FN; jn++)
+                            for (int x = 0; x < 4; x++) v[x] = v[x] < 0.f ? 0.f : v[x];
+                        }
+                        if (g.mask) {
+                            const f32x4 mk = *reinterpret_cast<const f32x4 *>(g.mask + o0 + idx);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int64_t idx = o0 + (int64_t)(rbase + i * 16 + r) * g.ldo + cbase + jn * 16;
-                        float v = acc[i][jn][r];
-                        if (g.bias) v += bv[jn];
-                        if ((g.flags & F_RELU) && v < 0.f) v = 0.f;
-                        if (g.mask && g.mask[idx] <= 0.f) v = 0.f;
-                        if (g.res) v += g.res[idx];
-                        if (g.flags & F_ACC) v += g.out[idx];
-                        g.out[idx] = v;
+                            for (int x = 0; x < 4; x++)
+                                if (mk[x] <= 0.f) v[x] = 0.f;
+                        }
+                        if (g.res) v += *reinterpret_cast<const f32x4 *>(g.res + o0 + idx);
+                        if (g.flags & F_ACC) v += *reinterpret_cast<const f32x4 *>(obase + idx);
                     }
+                    *reinterpret_cast<f32x4 *>(obase + idx) = v;
+                }
+            }
         }
 
         vb += cur.nst;
@@ -381,6 +397,7 @@ bool group_eligible(const DmaGemm &d) {
     if (!al16(d.a) || !al16(d.b) || !al16(d.out) || (d.mask && !al16(d.mask)) || (d.res && !al16(d.res)))
         return false;
     if (d.lda % 4 || d.ldb % 4 || d.a_stride % 4 || d.a_inner % 4 || d.b_stride % 4 || d.b_inner % 4) return false;
+    if (d.ldo % 4 || d.o_stride % 4 || d.o_inner % 4) return false;
     if (!fits32(d.lda) || !fits32(d.ldb) || !fits32(d.ldo) || !fits32(d.a_group) || !fits32(d.b_group) ||
         !fits32(d.o_group))
         return false;
