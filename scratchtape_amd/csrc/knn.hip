@@ -140,33 +140,53 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Sorts buf[0..n) ascending (n a power of two) within one wave: LDS operations
-// of a wave complete in order, so the stages need no barrier, only a fence that
-// keeps the compiler from reordering them.
-__device__ void wave_sort(uint64_t *buf, int n, int lane) {
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = lane; i < n; i += 64) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = buf[i], b = buf[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((a > b) == up) {
-                        buf[i] = b;
-                        buf[ixj] = a;
-                    }
-                }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic networks over the 64 R keys of one wave held in registers: element
+// e = 64 r + lane sits in lane `lane`, register r.  Exchanges across lanes
+// (distance < 64) are shuffles, across registers (distance >= 64) swaps
+// within the lane.  One pass (k, j) orders each pair (e, e ^ j) ascending when
+// e & k == 0, descending otherwise.
+template <int R, int K, int J>
+__device__ __forceinline__ void bitonic_pass(uint64_t (&x)[R], int lane) {
+    if constexpr (J >= 64) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if ((r & (J / 64)) == 0) {
+                const int p = r | (J / 64);
+                const bool asc = ((r * 64) & K) == 0;
+                const uint64_t a = x[r], b = x[p];
+                const uint64_t lo = a < b ? a : b, hi = a < b ? b : a;
+                x[r] = asc ? lo : hi;
+                x[p] = asc ? hi : lo;
             }
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            __builtin_amdgcn_wave_barrier();
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t y = shfl_xor_u64(x[r], J);
+            const bool asc = ((r * 64 + lane) & K) == 0;
+            const bool take_min = ((lane & J) == 0) == asc;
+            x[r] = (take_min == (x[r] < y)) ? x[r] : y;
         }
     }
 }
 
-__device__ __forceinline__ int pow2_at_least(int x) {
-    int n = KMAX;
-    while (n < x) n <<= 1;
-    return n;
+// The passes j = J, J/2, .., 1 of stage K.
+template <int R, int K, int J>
+__device__ __forceinline__ void bitonic_stage(uint64_t (&x)[R], int lane) {
+    bitonic_pass<R, K, J>(x, lane);
+    if constexpr (J > 1) bitonic_stage<R, K, J / 2>(x, lane);
+}
+
+// Sorts the 64 R keys ascending (stages K = 2, 4, .., 64 R).
+template <int R, int K = 2>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&x)[R], int lane) {
+    bitonic_stage<R, K, K / 2>(x, lane);
+    if constexpr (K < 64 * R) bitonic_sort<R, 2 * K>(x, lane);
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
@@ -339,6 +359,43 @@ __device__ __forceinline__ void score_chunk(const Chunk &ch, const v8i (&aq)[2],
 
 constexpr int E8 = KMAX / SW;  // each wave's published rank: SW * E8 = KMAX keys
 
+typedef __attribute__((address_space(3))) uint64_t lds_u64;
+
+struct Kept {
+    int32_t na;    // keys kept (sorted at wl[0, na))
+    uint64_t tau;  // the 128th smallest kept key, NONE while fewer
+};
+
+// Merges a wave's nb new keys (wl[KMAX, KMAX + nb), nb <= 128) into its na
+// kept ones (wl[0, na), sorted): the new keys are sorted in registers, the
+// minimum of each kept key and the mirrored new key (a bitonic split) holds
+// the 128 smallest of both, and a bitonic merge sorts them into wl[0, KMAX).
+// The E8-th smallest goes to *e8 (when there are E8).  Not inlined: it runs a
+// few times per wave and query, and inlined its registers would spill the
+// scan loop's.
+__device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, int nb, lds_u64 *e8, int lane) {
+    uint64_t nk[2], kp[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) nk[r] = r * 64 + lane < nb ? wl[KMAX + r * 64 + lane] : NONE;
+    bitonic_sort<2>(nk, lane);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint64_t a = r * 64 + lane < na ? wl[r * 64 + lane] : NONE;
+        const uint64_t b = shfl_xor_u64(nk[1 - r], 63);  // new key 127 - (64 r + lane)
+        kp[r] = a < b ? a : b;
+    }
+    bitonic_stage<2, 128, 64>(kp, lane);
+    wl[lane] = kp[0];
+    wl[64 + lane] = kp[1];
+    if (lane == E8 - 1 && kp[0] != NONE) *e8 = kp[0];
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    Kept k;
+    k.na = __popcll(__ballot(kp[0] != NONE)) + __popcll(__ballot(kp[1] != NONE));
+    k.tau = ((uint64_t)__shfl((uint32_t)(kp[1] >> 32), 63, 64) << 32) | __shfl((uint32_t)kp[1], 63, 64);
+    return k;
+}
+
 // grid: one workgroup of 1024 threads per query.
 __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const float *scales,
                                                 const int64_t *__restrict__ cell_start, int64_t ncells,
@@ -359,6 +416,9 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t q = blockIdx.x;
+    const int64_t total = (int64_t)nq * nprobe;
+    const int32_t pv0 = tid < total ? probes[tid] : -1;
+    const int32_t pv1 = tid + STH < total ? probes[tid + STH] : -1;
 
     if (wave == 0) {
         const QInfo qi = quantize_query(queries + q * D, lane, s_Q);
@@ -388,14 +448,12 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         }
     }
     __syncthreads();
-    // How many (query, probe) pairs of the whole batch scan each probed cell.
-    {
-        const int64_t total = (int64_t)nq * nprobe;
-        for (int64_t i = tid; i < total; i += STH) {
-            const int32_t v = probes[i];
-            for (int j = 0; j < nprobe; j++)
-                if (v == s_cell[j]) atomicAdd(&s_share[j], 1);
-        }
+    // How many (query, probe) pairs of the whole batch scan each probed cell
+    // (the first two probe ids per thread were loaded before the barrier).
+    for (int64_t i = tid, it = 0; i < total; i += STH, it++) {
+        const int32_t v = it == 0 ? pv0 : it == 1 ? pv1 : probes[i];
+        for (int jj = 0; jj < nprobe; jj++)
+            if (v == s_cell[jj]) atomicAdd(&s_share[jj], 1);
     }
     __syncthreads();
     if (tid == 0) {
@@ -476,11 +534,17 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     // key, and the largest of the waves' published E8-th smallest keys (16
     // waves x 8 keys at or below it).  Their minimum over the workgroup lives
     // in s_tau, which only decreases.
+    // Each wave's list: wl[0, KMAX) holds its kept keys sorted ascending
+    // (na of them, then NONE or larger keys already dropped), wl[KMAX, CAPW)
+    // takes new keys (nb of them, at most 128).  Once more than 64 are
+    // waiting they are merged into the kept ones (merge_new_keys).
     uint64_t *wl = cand + wave * CAPW;
-    int wcount = 0;
+    int na = 0, nb = 0;
     uint64_t tau_w = NONE;
-    // Folds this wave's thresholds into s_tau and drops the (sorted) list's
-    // keys above the result.
+    wl[lane] = NONE;
+    wl[64 + lane] = NONE;
+    // Folds this wave's thresholds into s_tau and drops the kept keys above
+    // the result.
     auto refresh = [&]() {
         const uint64_t m = wave_max_u64(lane < SW ? s_e8[lane] : 0ull);
         const uint64_t t = tau_w < m ? tau_w : m;
@@ -488,21 +552,19 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         const uint64_t ts = __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const uint64_t cut = t < ts ? t : ts;
         int c = 0;
-        for (int i = 0; i < wcount; i += 64) c += __popcll(__ballot(i + lane < wcount && wl[i + lane] <= cut));
-        wcount = c;
+        for (int i = 0; i < na; i += 64) c += __popcll(__ballot(i + lane < na && wl[i + lane] <= cut));
+        na = c;
     };
     auto wave_compact = [&]() {
-        const int n = pow2_at_least(wcount);
-        for (int i = wcount + lane; i < n; i += 64) wl[i] = NONE;
-        wave_sort(wl, n, lane);
-        if (wcount >= KMAX) {
-            tau_w = wl[KMAX - 1];
-            wcount = KMAX;
+        if (nb > 0) {
+            const Kept k = merge_new_keys((lds_u64 *)wl, na, nb, (lds_u64 *)(s_e8 + wave), lane);
+            na = k.na;
+            nb = 0;
+            tau_w = k.tau;
         }
-        if (wcount >= E8 && lane == 0) s_e8[wave] = wl[E8 - 1];
         refresh();
     };
-    auto score = [&](const Chunk &ch) {
+    auto score = [&](const Chunk &ch, bool merge = true) {
         int32_t dq[4], n12;
         score_chunk(ch, aq, dq, n12);
         const int32_t duq = dq[0];
@@ -518,12 +580,12 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         const bool take = lane >= ch.lo && lane < ch.hi && k64 < tau;
         const uint64_t mask = __ballot(take);
         if (take) {
-            const int pos = wcount + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-            wl[pos] = k64;
+            const int pos = nb + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            wl[KMAX + pos] = k64;
         }
-        wcount += __popcll(mask);
-        if (wcount >= CAPW - 64) wave_compact();  // at most CAPW - 1 entries, sorted as CAPW
+        nb += __popcll(mask);
+        if (merge && nb > 64) wave_compact();  // at most 128 new keys
     };
 
     // Three chunks per wave in flight: while one is scored the next two load.
@@ -542,13 +604,12 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         fetch(small, x1);
         fetch(small, x2);
         asm volatile("" ::: "memory");
-        score(x0);
+        score(x0, false);
+        score(x1, false);
+        wave_compact();
         fetch(small, x0);
-        asm volatile("" ::: "memory");
-        score(x1);
         fetch(small, x1);
         asm volatile("" ::: "memory");
-        wave_compact();
         __syncthreads();
         refresh();
         // Phase B: the rest, three chunks per trip (x2, x0, x1 hold this
@@ -582,7 +643,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         const uint64_t m = wave_max_u64(lane < SW ? s_e8[lane] : 0ull);
         const uint64_t ts = s_tau;
         const uint64_t tfin = m < ts ? m : ts;
-        for (int i = lane; i < wcount; i += 64) {
+        for (int i = lane; i < na; i += 64) {
             const uint64_t e = wl[i];
             if (e <= tfin) fin[atomicAdd(&count, 1)] = e;
         }
