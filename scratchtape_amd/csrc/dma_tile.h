@@ -49,6 +49,65 @@ __device__ __forceinline__ void dma16(const float *gptr, uint32_t lds_addr) {
         : "memory");
 }
 
+// One k-stage's DMA of one wave for the grouped GEMM: LA loads of operand A
+// from abase + ao[i] into LDS m0a + 1024 i, then LB of B from bbase + bo[i]
+// into m0b + 1024 i (bases wave-uniform in SGPRs, per-lane byte offsets in
+// VGPRs).  The instruction offset 1024 i is added to both the global and the
+// LDS address, so ao[i] / bo[i] are the source offsets minus 1024 i and M0 is
+// written once per operand; one wait state separates each M0 write from the
+// loads that read it, and M0 is restored at the end.
+template <int LA, int LB>
+__device__ __forceinline__ void dma_stage(const void *abase, const uint32_t (&ao)[LA], uint32_t m0a,
+                                          const void *bbase, const uint32_t (&bo)[LB], uint32_t m0b);
+
+template <>
+__device__ __forceinline__ void dma_stage<4, 4>(const void *abase, const uint32_t (&ao)[4], uint32_t m0a,
+                                                const void *bbase, const uint32_t (&bo)[4], uint32_t m0b) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %9\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %10\n\t"
+        "global_load_lds_dwordx4 %2, %10 offset:1024\n\t"
+        "global_load_lds_dwordx4 %3, %10 offset:2048\n\t"
+        "global_load_lds_dwordx4 %4, %10 offset:3072\n\t"
+        "s_mov_b32 m0, %11\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %5, %12\n\t"
+        "global_load_lds_dwordx4 %6, %12 offset:1024\n\t"
+        "global_load_lds_dwordx4 %7, %12 offset:2048\n\t"
+        "global_load_lds_dwordx4 %8, %12 offset:3072\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(ao[0]), "v"(ao[1]), "v"(ao[2]), "v"(ao[3]), "v"(bo[0]), "v"(bo[1]), "v"(bo[2]), "v"(bo[3]), "s"(m0a),
+          "s"(abase), "s"(m0b), "s"(bbase)
+        : "memory");
+}
+
+template <>
+__device__ __forceinline__ void dma_stage<4, 2>(const void *abase, const uint32_t (&ao)[4], uint32_t m0a,
+                                                const void *bbase, const uint32_t (&bo)[2], uint32_t m0b) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %7\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %8\n\t"
+        "global_load_lds_dwordx4 %2, %8 offset:1024\n\t"
+        "global_load_lds_dwordx4 %3, %8 offset:2048\n\t"
+        "global_load_lds_dwordx4 %4, %8 offset:3072\n\t"
+        "s_mov_b32 m0, %9\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %5, %10\n\t"
+        "global_load_lds_dwordx4 %6, %10 offset:1024\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(ao[0]), "v"(ao[1]), "v"(ao[2]), "v"(ao[3]), "v"(bo[0]), "v"(bo[1]), "s"(m0a), "s"(abase), "s"(m0b),
+          "s"(bbase)
+        : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_addr_of(const float *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
 }

@@ -85,9 +85,9 @@ struct Unit {
     int32_t nst, row0, col0, slice;
     int64_t zb;
     bool akc, bkc;
-    const float *abase, *bbase;
-    int64_t aoff[C::LA], boff[C::LB];
-    int64_t astep, bstep;
+    const char *anext, *bnext;          // operand bytes of the next stage to issue (wave-uniform)
+    int64_t astep, bstep;               // bytes per stage
+    uint32_t aoff[C::LA], boff[C::LB];  // this lane's DMA source offsets, less the instruction offsets
 };
 
 template <int ROWS>
@@ -124,18 +124,22 @@ __device__ void locate(const GroupArgs &ga, int x, int j, int wave, int lane, Un
     u.nst = (min(g.k, kbeg + g.slice_k) - kbeg) / BK;
     u.akc = !(g.flags & F_TA);
     u.bkc = (g.flags & F_TB) != 0;
-    u.abase = g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner);
-    u.bbase = g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner);
+    u.anext = reinterpret_cast<const char *>(g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner) +
+                                             (u.akc ? kbeg : (int64_t)kbeg * g.lda));
+    u.bnext = reinterpret_cast<const char *>(g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner) +
+                                             (u.bkc ? kbeg : (int64_t)kbeg * g.ldb));
+    // Wave-load i of this wave fills LDS 1024 i bytes after the wave's first;
+    // its sources lie at least 1024 i bytes past the base (rows >= 8 i apart
+    // at ld >= 32, or k-lines >= i apart at ld >= 256; the leading dimensions
+    // are checked on the host), so the offsets stay non-negative.
 #pragma unroll
     for (int i = 0; i < C::LA; i++)
-        u.aoff[i] = slot_src_rt<C::TM>(u.akc, (wave * C::LA + i) * 64 + lane, g.lda, u.row0) +
-                    (u.akc ? kbeg : (int64_t)kbeg * g.lda);
+        u.aoff[i] = (uint32_t)(4 * slot_src_rt<C::TM>(u.akc, (wave * C::LA + i) * 64 + lane, g.lda, u.row0) - 1024 * i);
 #pragma unroll
     for (int i = 0; i < C::LB; i++)
-        u.boff[i] = slot_src_rt<TN>(u.bkc, (wave * C::LB + i) * 64 + lane, g.ldb, u.col0) +
-                    (u.bkc ? kbeg : (int64_t)kbeg * g.ldb);
-    u.astep = u.akc ? BK : (int64_t)BK * g.lda;
-    u.bstep = u.bkc ? BK : (int64_t)BK * g.ldb;
+        u.boff[i] = (uint32_t)(4 * slot_src_rt<TN>(u.bkc, (wave * C::LB + i) * 64 + lane, g.ldb, u.col0) - 1024 * i);
+    u.astep = 4 * (u.akc ? BK : (int64_t)BK * g.lda);
+    u.bstep = 4 * (u.bkc ? BK : (int64_t)BK * g.ldb);
 }
 
 // grid: a multiple of 8 workgroups, at most one per CU (the ring takes most
@@ -157,18 +161,20 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
     if (cur.p < 0) return;
     locate(ga, x, j + L, wave, lane, nxt);
 
-    auto issue = [&](const Unit<C> &u, int st, int vst) {
-        const uint32_t base = lds_addr_of(lds + (vst % NS) * (SA + SB));
-#pragma unroll
-        for (int i = 0; i < LA; i++) dma16(u.abase + u.aoff[i] + st * u.astep, base + (wave_u * LA + i) * 1024);
-#pragma unroll
-        for (int i = 0; i < LB; i++)
-            dma16(u.bbase + u.boff[i] + st * u.bstep, base + SA * 4 + (wave_u * LB + i) * 1024);
+    // The ring advances one slot per stage: islot is the byte offset of the
+    // slot the next issued stage fills, rslot of the next stage to land.
+    constexpr uint32_t SLOT = (SA + SB) * 4;
+    const uint32_t lds0 = lds_addr_of(lds);
+    uint32_t islot = 0, rslot = 0;
+    auto issue = [&](Unit<C> &u) {
+        const uint32_t m0a = lds0 + islot + wave_u * LA * 1024;
+        dma_stage<LA, LB>(u.anext, u.aoff, m0a, u.bnext, u.boff, lds0 + islot + SA * 4 + wave_u * LB * 1024);
+        u.anext += u.astep;
+        u.bnext += u.bstep;
+        islot = islot + SLOT == NS * SLOT ? 0 : islot + SLOT;
     };
-
-    int vb = 0;  // ring position (virtual stage number) of cur's stage 0
 #pragma unroll
-    for (int st = 0; st < NS - 1; st++) issue(cur, st, st);
+    for (int st = 0; st < NS - 1; st++) issue(cur);
 
     f32x4 acc[FM][FN];
     while (true) {
@@ -193,12 +199,12 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                 const int issued = more ? st + NS - 1 : min(st + NS - 1, nst);
                 wait_stage<LA + LB, NS - 2>(issued - st - 1);
                 bar();
-                const int is = st + NS - 1;
-                if (is < nst)
-                    issue(cur, is, vb + is);
+                if (st + NS - 1 < nst)
+                    issue(cur);
                 else if (more)
-                    issue(nxt, is - nst, vb + is);
-                const float *la = lds + ((vb + st) % NS) * (SA + SB);
+                    issue(nxt);
+                const float *la = lds + rslot / 4;
+                rslot = rslot + SLOT == NS * SLOT ? 0 : rslot + SLOT;
                 const float *lb = la + SA;
                 const int gq = lane >> 4;
                 if constexpr (F16) {
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
         bar();
         {
             constexpr int EP = WN + 4;
-            float *ep = lds + ((vb + cur.nst - 1) % NS) * (SA + SB) + wave * 16 * EP;
+            float *ep = lds + (rslot == 0 ? NS * SLOT : rslot) / 4 - (SA + SB) + wave * 16 * EP;
             const bool split = g.splits > 1;
             float *const P = split ? g.out + (cur.zb * g.splits + cur.slice) * (int64_t)g.m * g.n : nullptr;
             const int64_t o0 = split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner);
@@ -319,7 +325,6 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
             }
         }
 
-        vb += cur.nst;
         if (nxt.p < 0) break;
         cur = nxt;
         j += L;
@@ -398,6 +403,7 @@ bool group_eligible(const DmaGemm &d) {
         return false;
     if (d.lda % 4 || d.ldb % 4 || d.a_stride % 4 || d.a_inner % 4 || d.b_stride % 4 || d.b_inner % 4) return false;
     if (d.ldo % 4 || d.o_stride % 4 || d.o_inner % 4) return false;
+    if (d.lda < (d.ta ? d.m : d.k) || d.ldb < (d.tb ? d.k : d.n)) return false;
     if (!fits32(d.lda) || !fits32(d.ldb) || !fits32(d.ldo) || !fits32(d.a_group) || !fits32(d.b_group) ||
         !fits32(d.o_group))
         return false;
