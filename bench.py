@@ -495,9 +495,9 @@ def main():
         graph16 = t16["grouped"]["graph_ms"]
         value = ss16.flops / graph16 / 1e9
         # The dominant kernel is the grouped launch itself (k_gemm_group, plus the split-k sum k_sum_group):
-        # the set's flops and algorithmic bytes over its per-call time from HIP events on its stream.
+        # the set's flops and algorithmic bytes over its time per graph replay, from HIP events on its stream.
         roof = roofline("k_gemm_group f16 (+ k_sum_group): the 15-GEMM set in one grouped call", ss16.flops,
-                        ss16.bytes, t16["grouped"]["eager_ms"],
+                        ss16.bytes, graph16,
                         traffic_for("k_gemm_group f16 step set", "scratchtape_amd/csrc/gemm_group.hip"))
         extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes, graph_ms=graph16,
                                    tflops=round(value, 2), mfma_frac=round(value / PEAK["f16"], 4),
@@ -506,8 +506,8 @@ def main():
         g32 = t32["grouped"]["graph_ms"]
         v32 = ss32.flops / g32 / 1e9
         extra["c3_f32_set"] = dict(graph_ms=g32, tflops=round(v32, 2), mfma_frac=round(v32 / PEAK["f32"], 4),
-                                   roofline=roofline("k_gemm_group f32 (+ k_sum_group)", ss32.flops, ss32.bytes,
-                                                     t32["grouped"]["eager_ms"], route="f32"),
+                                   roofline=roofline("k_gemm_group f32 (+ k_sum_group)", ss32.flops, ss32.bytes, g32,
+                                                     route="f32"),
                                    modes=t32, per_gemm=calls32, parity_max_rel_err=err32)
         log("[bench] C1 / C2 tape forms")
         extra["c1_256cube_f32"] = bench_tape_forms(dev, stream, 256, 256, 256, False)
