@@ -169,6 +169,35 @@ st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *scales,
                                  int64_t nprobe, int64_t d, int64_t k, int64_t *out_idx,
                                  float *out_dist, st_stream stream);
 
+/* ---- IVF probe selection ---------------------------------------------------
+ * Scoring contract: centroids and queries are quantised as the scan quantises
+ * a query (int16 values X, power-of-two scale 2^e per vector, e = exponent of
+ * max|x| - 14); dd = cnorm - ldexp(sum Q C, qe + ce + 1) in float64 with the
+ * integer dot exact; cells ranked by (dd, cell id).  d == 256. */
+
+/* Bytes of the digit store st_knn_centroids_prep writes for nlist centroids
+ * (4096 per block of 8), or -1 for a width other than 256. */
+int64_t st_knn_centroid_digit_bytes(int64_t nlist, int64_t d);
+
+/* gpu_step/knn/ivf.rs:62-69 `Cent::new`: centroids [nlist, d] f32 (device) ->
+ * digits (st_knn_centroid_digit_bytes bytes, 16-byte aligned; the quantised
+ * centroids as int8 digit planes laid out for the matrix cores), cexp
+ * [nlist] int32 scale exponents and cnorm [nlist] float64 squared norms of the
+ * quantised centroids. */
+st_status st_knn_centroids_prep(const float *centroids, int64_t nlist, int64_t d, int8_t *digits,
+                                int32_t *cexp, double *cnorm, st_stream stream);
+
+/* gpu_step/knn/ivf.rs:473-489 (the probe stage of `search_ivf`) and
+ * ivf.rs:128-161 `k_probe`: for queries [nq, d] f32, probes [nq, nprobe]
+ * int32 = each query's nprobe (1..=min(nlist, 16), PROBE_MAX ivf.rs:126)
+ * nearest cells by (dd, cell id), nearest first.  digits/cexp/cnorm as
+ * written by st_knn_centroids_prep.  Uses the library's kNN scratch arena
+ * (float64 dd of up to 256 MiB per chunk of queries): calls that overlap on
+ * one device race on it. */
+st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, const double *cnorm, int64_t nlist,
+                       const float *queries, int64_t nq, int64_t d, int64_t nprobe, int32_t *probes,
+                       st_stream stream);
+
 /* Benchmark support, no reference counterpart: fills rows [row0, row0 + n)
  * of a synthetic 2-bit store with keys drawn N(0,1) from a counter-based
  * generator (seed, global row, component) and quantised as

@@ -31,6 +31,13 @@ knn_prep_query         build contract (int16 query)               exactness: Q*q
 knn_search             build contract (ivf.rs:235 distance,       int64 brute force + numpy float32 formula + lexsort;
                        ivf.rs:673-684 finalisation)               exact integer dot vs float64; fidelity to the
                                                                    reference's own f16 scoring within its 2e-3 tolerance
+knn_centroid_prep      ivf.rs:62-69 Cent::new, with the scan's     exactness: C * 2^cexp reproduces the centroid as
+                       int16 quantiser in place of f16 rounding  knn_prep_query does; cnorm = float64 |C 2^cexp|^2
+knn_probe              ivf.rs:128-161 k_probe over the dots of     float64 brute force of |q - c|^2 (ranking agrees
+                       ivf.rs:473-484                             wherever the gap exceeds the quantisation bound); a
+                                                                   query equal to a centroid probes it first; duplicate
+                                                                   centroids tie to the lower id; permutation covariance;
+                                                                   nprobe = nlist is a full sort
 =====================  =========================================  ======================================================
 """
 from __future__ import annotations
@@ -50,6 +57,7 @@ _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 _i16p = np.ctypeslib.ndpointer(dtype=np.int16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _u64 = ctypes.c_uint64
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -99,6 +107,8 @@ def lib():
         L.orc_knn_dists.argtypes = [_u8p, _f32p, _i64, _i64, _i64, _i16p, ctypes.POINTER(QPrep), _f32p]
         L.orc_knn_search.argtypes = [_u8p, _f32p, _i64p, _f32p, _i32p, _i64, _i64, _i64, _i64, _i64p, _f32p]
         L.orc_knn_ref_f16_dist.argtypes = [_u8p, ctypes.c_float, ctypes.c_float, _f32p, _i64]
+        L.orc_knn_centroid_prep.argtypes = [_f32p, _i64, _i64, _i16p, _i32p, _f64p]
+        L.orc_knn_probe.argtypes = [_i16p, _i32p, _f64p, _i64, _f32p, _i64, _i64, _i64, _i32p]
         L.orc_knn_ref_f16_dist.restype = ctypes.c_float
         _lib = L
     return _lib
@@ -272,3 +282,25 @@ def knn_search(codes, scales, cell_start, queries, probes, k=128):
 def knn_ref_f16_dist(code_row, scale, norm_f16, q):
     return lib().orc_knn_ref_f16_dist(np.ascontiguousarray(code_row, np.uint8), float(scale), float(norm_f16),
                                       np.ascontiguousarray(q, np.float32), q.size)
+
+
+def knn_centroid_prep(cent: np.ndarray):
+    """Centroids [nlist, d] f32 -> (C int16 [nlist, d], cexp int32 [nlist], cnorm float64 [nlist])."""
+    cent = np.ascontiguousarray(cent, np.float32)
+    nlist, d = cent.shape
+    C = np.empty((nlist, d), np.int16)
+    cexp = np.empty(nlist, np.int32)
+    cnorm = np.empty(nlist, np.float64)
+    lib().orc_knn_centroid_prep(cent.reshape(-1), nlist, d, C.reshape(-1), cexp, cnorm)
+    return C, cexp, cnorm
+
+
+def knn_probe(cent: np.ndarray, queries: np.ndarray, nprobe: int, prep=None) -> np.ndarray:
+    """Each query's nprobe nearest cells by (dd, cell id), nearest first: int32 [nq, nprobe]."""
+    C, cexp, cnorm = prep if prep is not None else knn_centroid_prep(cent)
+    queries = np.ascontiguousarray(queries, np.float32)
+    nq, d = queries.shape
+    out = np.empty((nq, nprobe), np.int32)
+    lib().orc_knn_probe(np.ascontiguousarray(C).reshape(-1), cexp, cnorm, C.shape[0], queries.reshape(-1), nq, d,
+                        nprobe, out.reshape(-1))
+    return out

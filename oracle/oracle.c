@@ -517,3 +517,61 @@ float orc_knn_ref_f16_dist(const uint8_t *code, float s, float norm_f16, const f
     }
     return qn + norm_f16 - 2.0f * dot;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Probe selection: each query's nprobe nearest IVF cells.                   */
+/* ------------------------------------------------------------------------ */
+
+/* The centroid side of probe selection (ivf.rs:62-69 `Cent::new`, with the
+ * integer contract of the scan in place of f16 rounding): centroid c is
+ * quantised exactly as a query (orc_knn_prep_query), C[c] = its int16 values,
+ * cs = 2^cexp[c] its power-of-two scale, and cnorm[c] = |C cs|^2 =
+ * ldexp(sum C^2, 2 cexp) in float64 (exact: sum C^2 < 2^37). */
+void orc_knn_centroid_prep(const float *cent, int64_t nlist, int64_t d, int16_t *C, int32_t *cexp,
+                           double *cnorm) {
+    for (int64_t c = 0; c < nlist; c++) {
+        orc_qprep p;
+        orc_knn_prep_query(cent + c * d, d, C + c * d, &p);
+        int64_t s2 = 0;
+        for (int64_t i = 0; i < d; i++) s2 += (int64_t)C[c * d + i] * C[c * d + i];
+        cexp[c] = ilogbf(p.qs);
+        cnorm[c] = ldexp((double)s2, 2 * cexp[c]);
+    }
+}
+
+/* ivf.rs:128-161 `k_probe` over the centroid dots of ivf.rs:473-484: for
+ * each query (quantised as in the scan: Q, qs = 2^qe) and centroid c,
+ *     dd = cnorm[c] - ldexp(dot, qe + cexp[c] + 1),   dot = sum Q_i C[c]_i
+ * (dot exact in int64, dd one float64 subtraction), and the nprobe smallest
+ * by (dd, c), nearest first, into probes [nq, nprobe]. */
+void orc_knn_probe(const int16_t *C, const int32_t *cexp, const double *cnorm, int64_t nlist,
+                   const float *queries, int64_t nq, int64_t d, int64_t nprobe, int32_t *probes) {
+    int16_t *Q = (int16_t *)malloc(sizeof(int16_t) * (size_t)d);
+    double *bd = (double *)malloc(sizeof(double) * (size_t)nprobe);
+    int32_t *bi = (int32_t *)malloc(sizeof(int32_t) * (size_t)nprobe);
+    for (int64_t qi = 0; qi < nq; qi++) {
+        orc_qprep p;
+        orc_knn_prep_query(queries + qi * d, d, Q, &p);
+        const int qe = ilogbf(p.qs);
+        int64_t size = 0;
+        for (int64_t c = 0; c < nlist; c++) {
+            int64_t dot = 0;
+            const int16_t *cr = C + c * d;
+            for (int64_t i = 0; i < d; i++) dot += (int64_t)Q[i] * cr[i];
+            double dd = cnorm[c] - ldexp((double)dot, qe + cexp[c] + 1);
+            if (size == nprobe && !(dd < bd[nprobe - 1])) continue;
+            int64_t pos = size < nprobe ? size++ : nprobe - 1;
+            while (pos > 0 && bd[pos - 1] > dd) {
+                bd[pos] = bd[pos - 1];
+                bi[pos] = bi[pos - 1];
+                pos--;
+            }
+            bd[pos] = dd;
+            bi[pos] = (int32_t)c;
+        }
+        for (int64_t j = 0; j < nprobe; j++) probes[qi * nprobe + j] = j < size ? bi[j] : -1;
+    }
+    free(bi);
+    free(bd);
+    free(Q);
+}

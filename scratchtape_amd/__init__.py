@@ -8,7 +8,7 @@ Python mirrors of the reference interfaces they replace:
 - matmul.matmul_grouped: independent GEMMs in one launch          (gpu_step/tape.rs:324-347)
 - tensor.ndarray_matmul                                         (src/tensor.rs NdArray::matmul)
 - rows.softmax / softmax_backward                               (gpu_step/rows.rs)
-- knn.KnnStore2bit / quantize_2bit                              (gpu_step/knn.rs, knn/ivf.rs)
+- knn.KnnStore2bit / quantize_2bit / Centroids                  (gpu_step/knn.rs, knn/ivf.rs)
 """
 from ._lib import ScratchtapeError, lib  # noqa: F401
 from .matmul import (Epilogue, MatRef, f16_enabled, f16_route, matmul, matmul_f32, matmul_grouped,  # noqa: F401

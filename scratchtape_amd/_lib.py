@@ -66,11 +66,15 @@ SIGNATURES = {
     "st_knn_search_ivf_2bit": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_store_2bit": [_u64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_keys_f32": [_u64, _i64, _i64, _i64, _vp, _vp],
+    "st_knn_centroid_digit_bytes": [_i64, _i64],
+    "st_knn_centroids_prep": [_vp, _i64, _i64, _vp, _vp, _vp, _vp],
+    "st_knn_probe": [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp],
     "st_last_error": [],
     "st_sync": [_vp],
     "st_version": [],
 }
-_RESTYPES = {"st_last_error": ctypes.c_char_p, "st_version": ctypes.c_char_p, "st_f16_enabled": _i32}
+_RESTYPES = {"st_last_error": ctypes.c_char_p, "st_version": ctypes.c_char_p, "st_f16_enabled": _i32,
+             "st_knn_centroid_digit_bytes": _i64}
 
 _lib = None
 

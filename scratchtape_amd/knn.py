@@ -7,6 +7,11 @@ ivf.rs:386-432), one f32 scale per key, codes packed 4 per byte.  The search
 takes each query's probed cells and returns, per query, the k nearest keys by
 the exact 2-bit score, ascending by (distance, key index), as global row
 indices with distances max(|q^|^2 + dist, 0) (ivf.rs:673-684).
+
+Probe selection (ivf.rs:62-69 `Cent`, ivf.rs:128-161 `k_probe`, the probe stage
+of `search_ivf` ivf.rs:473-489) runs on the device too: `Centroids` holds the
+quantised centroids, and `search_ivf(queries, nprobe)` picks each query's
+nprobe nearest cells by the exact integer distance before scanning them.
 """
 from __future__ import annotations
 
@@ -54,6 +59,43 @@ def synth_keys_f32(seed: int, row0: int, n: int, d: int = 256, device="cuda", st
     return keys
 
 
+class Centroids:
+    """The IVF centroids on the device, quantised for probe selection (ivf.rs:54-69 `Cent`).
+
+    digits: int8 digit planes (st_knn_centroid_digit_bytes bytes), cexp [nlist] int32,
+    cnorm [nlist] float64 (squared norms of the quantised centroids).
+    """
+
+    def __init__(self, centroids: torch.Tensor, stream=None):
+        if centroids.dim() != 2:
+            raise ValueError("centroids must be [nlist, d]")
+        nlist, d = centroids.shape
+        nbytes = int(_lib.lib().st_knn_centroid_digit_bytes(nlist, d))
+        if nbytes < 0:
+            raise ValueError(f"probe selection is built for d == 256 (got {d})")
+        dev = centroids.device
+        self.nlist, self.d = nlist, d
+        self.digits = torch.empty(nbytes, dtype=torch.int8, device=dev)
+        self.cexp = torch.empty(nlist, dtype=torch.int32, device=dev)
+        self.cnorm = torch.empty(nlist, dtype=torch.float64, device=dev)
+        _lib.call("st_knn_centroids_prep", _dptr(centroids, torch.float32, "centroids"), nlist, d,
+                  self.digits.data_ptr(), self.cexp.data_ptr(), self.cnorm.data_ptr(), _stream(stream))
+
+    def probe(self, queries: torch.Tensor, nprobe: int, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """Each query's nprobe nearest cells, nearest first (ties to the lower id): int32 [nq, nprobe]."""
+        nq, d = queries.shape
+        if d != self.d:
+            raise ValueError(f"queries have width {d}, the centroids {self.d}")
+        if out is None:
+            out = torch.empty((nq, nprobe), dtype=torch.int32, device=queries.device)
+        elif out.shape != (nq, nprobe):
+            raise ValueError("out must be [nq, nprobe]")
+        _lib.call("st_knn_probe", self.digits.data_ptr(), self.cexp.data_ptr(), self.cnorm.data_ptr(), self.nlist,
+                  _dptr(queries, torch.float32, "queries"), nq, d, nprobe, _dptr(out, torch.int32, "probes"),
+                  _stream(stream))
+        return out
+
+
 class KnnStore2bit:
     """A cell-contiguous 2-bit key store on the device.
 
@@ -76,6 +118,13 @@ class KnnStore2bit:
         self.ncells = cs.size - 1
         self.max_cell = int(np.diff(cs).max())
         self.cell_start_dev = torch.from_numpy(cs).to(codes.device)
+        self.centroids: Optional[Centroids] = None
+
+    def set_centroids(self, centroids: torch.Tensor, stream=None) -> None:
+        """Attaches the IVF centroids [ncells, d] (cell c's centroid at row c) for search_ivf by nprobe."""
+        if centroids.shape != (self.ncells, self.d):
+            raise ValueError(f"need one centroid per cell: [{self.ncells}, {self.d}]")
+        self.centroids = Centroids(centroids, stream=stream)
 
     @classmethod
     def from_keys(cls, keys: torch.Tensor, cell_start, stream=None) -> "KnnStore2bit":
@@ -86,12 +135,18 @@ class KnnStore2bit:
     def __len__(self) -> int:
         return self.codes.shape[0]
 
-    def search_ivf(self, queries: torch.Tensor, probes: torch.Tensor, k: int = KMAX,
+    def search_ivf(self, queries: torch.Tensor, probes, k: int = KMAX,
                    out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, stream=None):
         """Per query, the k nearest keys of its probed cells: (idx [nq, k] int64, dist [nq, k] float32).
 
-        queries [nq, d] float32, probes [nq, nprobe] int32 cell ids (device tensors).
+        queries [nq, d] float32 (device); probes either [nq, nprobe] int32 cell ids (device) or an
+        int nprobe, in which case each query probes its nprobe nearest cells (set_centroids first),
+        as the reference's search_ivf(queries, rows, nprobe) does.
         """
+        if isinstance(probes, int):
+            if self.centroids is None:
+                raise ValueError("search_ivf by nprobe needs set_centroids")
+            probes = self.centroids.probe(queries, probes, stream=stream)
         nq, d = queries.shape
         if d != self.d:
             raise ValueError(f"queries have width {d}, the store {self.d}")

@@ -79,3 +79,25 @@ def test_f16_route_mirrors_the_reference_pick():
     assert not f16_route(64, 48, 64)          # k not a multiple of 32
     assert not f16_route(64, 64, 64, col_sum=True, b_trans=True)
     assert f16_route(4096, 256, 768)
+
+
+def test_probe_arguments_are_validated_like_the_reference_asserts():
+    # ivf.rs:469 asserts nprobe in 1..=min(nlist, PROBE_MAX); the width is the scan's 256.
+    L = scratchtape_amd.lib()
+    fake = 1 << 20  # aligned non-null stand-in: every call below is rejected before any access
+    assert L.st_knn_centroid_digit_bytes(12288, 256) == 1536 * 4096
+    assert L.st_knn_centroid_digit_bytes(9, 256) == 2 * 4096
+    assert L.st_knn_centroid_digit_bytes(9, 128) == -1
+    cases = [
+        ((None, fake, fake, 64, fake, 4, 256, 8, fake, None), b"NULL"),
+        ((fake, fake, fake, 64, fake, 4, 128, 8, fake, None), b"d == 256"),
+        ((fake, fake, fake, 64, fake, 4, 256, 17, fake, None), b"nprobe"),
+        ((fake, fake, fake, 64, fake, 4, 256, 0, fake, None), b"nprobe"),
+        ((fake, fake, fake, 4, fake, 4, 256, 5, fake, None), b"nprobe"),
+        ((fake, fake, fake, 64, fake + 4, 4, 256, 8, fake, None), b"aligned"),
+    ]
+    for args, msg in cases:
+        assert L.st_knn_probe(*args) == _lib.ST_ERR_INVALID
+        assert msg in L.st_last_error(), (args, L.st_last_error())
+    assert L.st_knn_centroids_prep(fake, 64, 200, fake, fake, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_knn_centroids_prep(fake, 0, 256, fake, fake, fake, None) == _lib.ST_ERR_INVALID

@@ -439,3 +439,104 @@ def test_knn_integer_dot_is_exact_and_close_to_the_references_f16_scoring():
         ref = oracle.knn_ref_f16_dist(codes[r], scales[r], norms[r], q)
         ours = float(prep.qn) + float(dists[r])
         assert abs(ours - ref) < 2e-3 * (1 + abs(ref))
+
+
+# --------------------------------------------------------------------------- probe selection
+
+
+def _dequantised(x):
+    """x [n, d] f32 -> each row as the scan's quantiser represents it, in float64 (exact)."""
+    out = np.empty(x.shape, np.float64)
+    for i, row in enumerate(x):
+        Q, prep = oracle.knn_prep_query(row)
+        out[i] = Q.astype(np.float64) * float(prep.qs)
+    return out
+
+
+def _rank(d2, nprobe):
+    """The nprobe smallest of each row of d2 by (value, column), as int32."""
+    cols = np.arange(d2.shape[1])
+    return np.stack([np.lexsort((cols, row))[:nprobe] for row in d2]).astype(np.int32)
+
+
+def test_centroid_prep_is_the_query_quantiser_with_exact_norms():
+    rng = np.random.default_rng(21)
+    cent = rng.standard_normal((40, 256)).astype(np.float32)
+    cent[3] = 0.0
+    cent[7] *= np.float32(2.0 ** -30)
+    cent[9] *= np.float32(2.0 ** 30)
+    C, cexp, cnorm = oracle.knn_centroid_prep(cent)
+    for c in range(40):
+        Q, prep = oracle.knn_prep_query(cent[c])
+        np.testing.assert_array_equal(C[c], Q)
+        assert 2.0 ** int(cexp[c]) == float(prep.qs)
+    deq = C.astype(np.float64) * np.exp2(cexp.astype(np.float64))[:, None]
+    np.testing.assert_array_equal(cnorm, (deq ** 2).sum(1))  # every term and partial sum is exact
+    assert cnorm[3] == 0.0 and cexp[3] == 0
+    rel = np.abs(cnorm - (cent.astype(np.float64) ** 2).sum(1)) / np.maximum((cent.astype(np.float64) ** 2).sum(1), 1e-300)
+    assert np.all(rel[np.arange(40) != 3] < 2.0 ** -11)
+
+
+@pytest.mark.parametrize("scale_spread", [False, True])
+def test_probe_ranks_by_the_dequantised_distance(scale_spread):
+    rng = np.random.default_rng(22)
+    nlist, nq, d, nprobe = 300, 24, 256, 16
+    cent = rng.standard_normal((nlist, d)).astype(np.float32)
+    if scale_spread:  # centroid and query magnitudes from 2^-40 to 2^40
+        cent *= np.exp2(rng.integers(-40, 41, nlist)).astype(np.float32)[:, None]
+    queries = rng.standard_normal((nq, d)).astype(np.float32)
+    if scale_spread:
+        queries *= np.exp2(rng.integers(-40, 41, nq)).astype(np.float32)[:, None]
+    probes = oracle.knn_probe(cent, queries, nprobe)
+    qh, ch = _dequantised(queries), _dequantised(cent)
+    d2 = ((qh[:, None, :] - ch[None, :, :]) ** 2).sum(2)  # |q^ - c^|^2, a different expression of the same order
+    want = _rank(d2, nprobe)
+    # Rows whose float64 sums leave a near-tie ambiguous are rare; none at this seed.
+    np.testing.assert_array_equal(probes, want)
+
+
+def test_probe_agrees_with_unquantised_distance_where_the_gap_is_clear():
+    rng = np.random.default_rng(23)
+    nlist, nq, d, nprobe = 500, 40, 256, 8
+    cent = rng.standard_normal((nlist, d)).astype(np.float32)
+    queries = (cent[rng.integers(0, nlist, nq)] + 0.7 * rng.standard_normal((nq, d))).astype(np.float32)
+    probes = oracle.knn_probe(cent, queries, nprobe)
+    true = ((queries.astype(np.float64)[:, None, :] - cent.astype(np.float64)[None]) ** 2).sum(2)
+    checked = 0
+    for i in range(nq):
+        srt = np.sort(true[i])
+        if srt[nprobe] - srt[nprobe - 1] > 1e-2:  # the quantisation moves d2 by < 1e-2 here
+            assert set(probes[i]) == set(np.argsort(true[i])[:nprobe])
+            checked += 1
+    assert checked > nq // 2
+
+
+def test_probe_query_equal_to_a_centroid_and_duplicate_centroids():
+    rng = np.random.default_rng(24)
+    cent = rng.standard_normal((64, 256)).astype(np.float32)
+    cent[40] = cent[5]
+    cent[50] = cent[5]
+    queries = np.stack([cent[17], cent[5], cent[5] + 1e-3 * rng.standard_normal(256).astype(np.float32)])
+    p = oracle.knn_probe(cent, queries, 4)
+    assert p[0, 0] == 17
+    assert list(p[1, :3]) == [5, 40, 50]  # equal dd: the lower id first
+    assert list(p[2, :3]) == [5, 40, 50]
+    assert list(oracle.knn_probe(cent, queries, 2)[1]) == [5, 40]
+
+
+def test_probe_is_covariant_under_centroid_permutation_and_full_sort_at_nprobe_nlist():
+    rng = np.random.default_rng(25)
+    nlist = 16
+    cent = rng.standard_normal((nlist, 256)).astype(np.float32)
+    queries = rng.standard_normal((10, 256)).astype(np.float32)
+    perm = rng.permutation(nlist)
+    p = oracle.knn_probe(cent, queries, 5)
+    pp = oracle.knn_probe(cent[perm], queries, 5)
+    np.testing.assert_array_equal(perm[pp], p)
+    full = oracle.knn_probe(cent, queries, nlist)
+    for row in full:
+        assert sorted(row) == list(range(nlist))
+    # A zero query ranks the cells by centroid norm (then id).
+    _, _, cnorm = oracle.knn_centroid_prep(cent)
+    z = oracle.knn_probe(cent, np.zeros((1, 256), np.float32), nlist)
+    np.testing.assert_array_equal(z[0], np.lexsort((np.arange(nlist), cnorm)))
