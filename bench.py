@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import contextlib
 import hashlib
+import itertools
 import json
 import os
 import platform
@@ -31,7 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "GEMM TFLOP/s + % MFMA peak at d_model-256 step shapes; kNN keys/s + % HBM BW"
-PEAK = {"f16": 2500.0, "f32": 157.3, "hbm_gbs": 8000.0}  # MI355X dense TFLOP/s, HBM GB/s
+PEAK = {"f16": 2500.0, "f32": 157.3, "i8": 5000.0, "hbm_gbs": 8000.0}  # MI355X dense TFLOP/s (i8: TOP/s), HBM GB/s
 T_TOKENS = 4096
 LAYERS = [("qkv", 256, 768), ("out", 256, 256), ("ffn1", 256, 1024), ("ffn2", 1024, 256), ("head", 256, 256)]
 
@@ -444,6 +445,57 @@ class KnnBench:
                            "no CPU quantised scorer")
 
 
+class ProbeBench:
+    """IVF probe selection at the scan benchmark's batch: 12288 centroids N(0,1), 256 queries, 8 probes each."""
+    NLIST, NQ, NPROBE, D = 12288, 256, 8, 256
+
+    def __init__(self, dev, queries, seed=77):
+        import torch
+        from scratchtape_amd import knn
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.cent = torch.randn((self.NLIST, self.D), generator=g, device=dev)
+        self.c = knn.Centroids(self.cent)
+        self.queries = queries
+        self.out = torch.empty((self.NQ, self.NPROBE), dtype=torch.int32, device=dev)
+        ncb, nqb = -(-self.NLIST // 8), -(-self.NQ // 8)
+        # Algorithmic bytes: the centroid store (512 B of digits + 12 B of exponent and norm per cell), the f32
+        # queries and the probe ids.  Matrix-core work: 4 k-steps of one 16x16x64 i8 MFMA per (query block,
+        # centroid block), i.e. the four digit products of every query-centroid dot.
+        self.bytes = self.NLIST * (512 + 12) + self.NQ * self.D * 4 + self.NQ * self.NPROBE * 4
+        self.ops = nqb * ncb * 4 * 2 * 16 * 16 * 64
+
+    def probe(self, i):
+        return self.c.probe(self.queries[i % len(self.queries)], self.NPROBE, out=self.out)
+
+    def run(self, stream, steps, warmup):
+        import torch
+        it = itertools.count()
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                self.probe(next(it))
+            torch.cuda.synchronize()
+            return time_events(lambda: self.probe(next(it)), steps, stream)
+
+    def check(self):
+        import oracle
+        got = self.probe(0).cpu().numpy()
+        return bool(np.array_equal(got, oracle.knn_probe(self.cent.cpu().numpy(), self.queries[0].cpu().numpy(),
+                                                         self.NPROBE)))
+
+    def cpu_baseline(self):
+        """The oracle's exact probe selection for one whole batch, 1 pinned thread."""
+        import oracle
+        prep = oracle.knn_centroid_prep(self.cent.cpu().numpy())
+        q = self.queries[1].cpu().numpy()
+        with one_core():
+            t0 = time.perf_counter()
+            oracle.knn_probe(None, q, self.NPROBE, prep=prep)
+            dt = time.perf_counter() - t0
+        return dict(value=round(self.NQ / dt, 1), unit="queries/s", cores=1, kind="port", seconds=round(dt, 3),
+                    sample=f"{self.NQ} queries x {self.NLIST} centroids x {self.NPROBE} probes (one batch): exact "
+                           "integer distances + top-8 in the oracle (C, 1 pinned thread)")
+
+
 # --------------------------------------------------------------------------- main
 
 def main():
@@ -554,6 +606,33 @@ def main():
         if not args.no_cpu:
             knn["cpu_baseline"] = kb.cpu_baseline()
         extra["c5_knn"] = knn
+        log("[bench] C5 probe selection (12288 centroids, 256 queries x 8)")
+        pb = ProbeBench(dev, [b["q"] for b in kb.batches])
+        pok = pb.check()
+        log(f"[bench] probe parity {'ok' if pok else 'FAILED'}")
+        if not pok:
+            log("[bench] PARITY FAILURE: refusing to report")
+            sys.exit(3)
+        pms = pb.run(stream, args.steps, args.warmup)
+        probe = dict(ms_per_batch=round(pms, 5), queries_per_s=round(pb.NQ / pms * 1e3, 1),
+                     roofline=roofline("st_knn_probe (k_probe_prep + k_probe_dots + k_probe_select)", pb.ops,
+                                       pb.bytes, pms,
+                                       traffic_for("st_knn_probe", "scratchtape_amd/csrc/knn_probe.hip"), route="i8"))
+        if not args.no_cpu:
+            probe["cpu_baseline"] = pb.cpu_baseline()
+        # search_ivf by nprobe: probe selection, then the scan of the selected cells (the store's cells are a
+        # uniform assignment, unrelated to these centroids: the timing, not the recall, is the point).
+        kb.store.centroids = pb.c
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                kb.store.search_ivf(kb.batches[i % 8]["q"], 8, 128, out=kb.out)
+            torch.cuda.synchronize()
+            it = itertools.count()
+            e2e = time_events(lambda: kb.store.search_ivf(kb.batches[next(it) % 8]["q"], 8, 128, out=kb.out),
+                              args.steps, stream)
+        probe["search_ivf_by_nprobe_ms_per_batch"] = round(e2e, 5)
+        extra["c5_knn_probe"] = probe
+        del pb
         if result is None:
             result = dict(metric=METRIC, value=knn["g_keys_per_s"], unit="G keys/s", n_gpus=1, steps=args.steps,
                           warmup=args.warmup, ms_per_step=knn["ms_per_batch"], higher_is_better=True,

@@ -25,9 +25,9 @@
 //   k_probe_prep   vectors -> digit blocks, exponent (and norm for centroids);
 //   k_probe_dots   dd for a chunk of queries x every centroid (float64, in the
 //                  library's scratch arena);
-//   k_probe_select one workgroup per query: per-thread sorted top-16 lists over
-//                  a strided share of the cells, then wave and workgroup
-//                  extract-min merges by (dd, id).
+//   k_probe_select one workgroup per query: a threshold from the per-thread
+//                  minima keeps about nprobe candidates per round of cells,
+//                  which one wave sorts by (dd, id).
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -181,6 +181,7 @@ __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ q
     }
 }
 
+// Order-preserving map of a float64 onto u64 (finite values; -0 < +0).
 __device__ __forceinline__ uint64_t dkey(double v) {
     const uint64_t x = (uint64_t)__double_as_longlong(v);
     return (x >> 63) ? ~x : (x | (1ull << 63));
@@ -190,12 +191,16 @@ __device__ __forceinline__ bool lt(uint64_t ka, int32_t ia, uint64_t kb, int32_t
     return ka < kb || (ka == kb && ia < ib);
 }
 
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // Wave-wide minimum of (key, id); every lane receives it.
 __device__ __forceinline__ void wave_min(uint64_t &k, int32_t &i) {
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t klo = __shfl_xor((uint32_t)k, o, 64), khi = __shfl_xor((uint32_t)(k >> 32), o, 64);
-        const uint64_t ko = ((uint64_t)khi << 32) | klo;
+        const uint64_t ko = shfl_xor_u64(k, o);
         const int32_t io = __shfl_xor(i, o, 64);
         if (lt(ko, io, k, i)) {
             k = ko;
@@ -204,91 +209,206 @@ __device__ __forceinline__ void wave_min(uint64_t &k, int32_t &i) {
     }
 }
 
+// Ascending bitonic sort of one u32 per lane across the wave.
+__device__ __forceinline__ uint32_t wave_sort_u32(uint32_t x, int lane) {
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t y = __shfl_xor(x, j, 64);
+            const bool take_min = ((lane & j) == 0) == ((lane & k) == 0);
+            x = take_min ? min(x, y) : max(x, y);
+        }
+    }
+    return x;
+}
+
+// Ascending bitonic sort of one (key, id) pair per lane across the wave.
+__device__ __forceinline__ void wave_sort_pair(uint64_t &k, int32_t &i, int lane) {
+#pragma unroll
+    for (int kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+            const uint64_t ko = shfl_xor_u64(k, j);
+            const int32_t io = __shfl_xor(i, j, 64);
+            const bool take_min = ((lane & j) == 0) == ((lane & kk) == 0);
+            if (take_min == lt(ko, io, k, i)) {
+                k = ko;
+                i = io;
+            }
+        }
+    }
+}
+
 constexpr uint64_t KNONE = ~0ull;
 constexpr int32_t INONE = 0x7fffffff;
+constexpr int SEL_T = 1024;         // threads per query
+constexpr int SEL_W = SEL_T / 64;   // waves
+constexpr int SEL_J = 12;           // cells per thread and round
+constexpr int SEL_ROUND = SEL_T * SEL_J;
+constexpr int CAND = 1024;          // LDS candidate buffer
 
-// One workgroup of 256 threads per query q of the chunk: probes[q][0, nprobe).
-__global__ __launch_bounds__(256) void k_probe_select(const double *__restrict__ dd, int32_t nlist, int32_t nprobe,
-                                                      int32_t *__restrict__ probes) {
-    __shared__ uint64_t s_k[4][PROBE_MAX];
-    __shared__ int32_t s_i[4][PROBE_MAX];
+// One workgroup of 1024 threads per query q of the chunk: probes[q][0, nprobe)
+// by (dd, id) ascending.  Rounds of 12288 cells: every thread loads its 12
+// values at once; a threshold on the high 32 bits of the ordered keys is the
+// nprobe-th smallest of the 1024 per-thread minima (so at least nprobe
+// candidates lie at or below it, and every member of the top nprobe does);
+// the candidates at or below it (about nprobe of them) and the running top
+// nprobe are collected in LDS and sorted by one wave.  Should the buffer
+// overflow (many equal distances), the round is re-read from memory by
+// nprobe successive minimum searches instead, which is exact for any input.
+__global__ __launch_bounds__(SEL_T) void k_probe_select(const double *__restrict__ dd, int32_t nlist, int32_t nprobe,
+                                                        int32_t *__restrict__ probes) {
+    __shared__ uint64_t s_ck[CAND];
+    __shared__ int32_t s_ci[CAND];
+    __shared__ uint32_t s_lm[SEL_W][PROBE_MAX];
+    __shared__ uint64_t s_bk[PROBE_MAX];
+    __shared__ int32_t s_bi[PROBE_MAX];
+    __shared__ uint32_t s_tau;
+    __shared__ int32_t s_cnt, s_nb;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t q = blockIdx.x;
     const double *row = dd + q * nlist;
+    if (tid == 0) s_nb = 0;
 
-    uint64_t bk[PROBE_MAX];
-    int32_t bi[PROBE_MAX];
+    for (int base = 0; base < nlist; base += SEL_ROUND) {
+        uint64_t key[SEL_J];
 #pragma unroll
-    for (int j = 0; j < PROBE_MAX; j++) {
-        bk[j] = KNONE;
-        bi[j] = INONE;
-    }
-    // Ascending cell ids per thread: a strictly smaller key displaces, so equal
-    // keys stay in id order.
-    for (int c0 = tid; c0 < nlist; c0 += 4 * 256) {
-        double v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int c = c0 + 256 * u;
-            v[u] = c < nlist ? row[c] : 0.0;
+        for (int j = 0; j < SEL_J; j++) {
+            const int c = base + j * SEL_T + tid;
+            key[j] = c < nlist ? dkey(row[c]) : KNONE;
         }
+        uint32_t m = 0xffffffffu;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int c = c0 + 256 * u;
-            const uint64_t key = dkey(v[u]);
-            if (c < nlist && key < bk[PROBE_MAX - 1]) {
+        for (int j = 0; j < SEL_J; j++) m = min(m, (uint32_t)(key[j] >> 32));
+        const uint32_t ms = wave_sort_u32(m, lane);
+        if (lane < nprobe) s_lm[w][lane] = ms;
+        __syncthreads();  // also orders the previous round's s_bk / s_nb before their use below
+        if (w == 0) {
+            // nprobe-th smallest of the 16 waves' nprobe smallest minima (the
+            // nprobe-th smallest of all 1024), and the running top's bound.
+            uint32_t v[4];
 #pragma unroll
-                for (int j = PROBE_MAX - 1; j > 0; j--) {
-                    const bool sh = bk[j - 1] > key;
-                    const bool here = !sh && bk[j] > key;
-                    bk[j] = sh ? bk[j - 1] : here ? key : bk[j];
-                    bi[j] = sh ? bi[j - 1] : here ? c : bi[j];
-                }
-                if (bk[0] > key) {
-                    bk[0] = key;
-                    bi[0] = c;
+            for (int r = 0; r < 4; r++) {
+                const int e = r * 64 + lane;
+                v[r] = e < SEL_W * nprobe ? s_lm[e / nprobe][e % nprobe] : 0xffffffffu;
+            }
+            uint32_t t = 0xffffffffu;
+            for (int r = 0; r < nprobe; r++) {
+                uint32_t lm = min(min(v[0], v[1]), min(v[2], v[3]));
+                uint32_t wm = lm;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) wm = min(wm, __shfl_xor(wm, o, 64));
+                t = wm;
+                // The lowest lane holding wm drops one copy of it.
+                const uint64_t holders = __ballot(lm == wm);
+                if (lane == __builtin_ctzll(holders)) {
+                    if (v[0] == wm) v[0] = 0xffffffffu;
+                    else if (v[1] == wm) v[1] = 0xffffffffu;
+                    else if (v[2] == wm) v[2] = 0xffffffffu;
+                    else v[3] = 0xffffffffu;
                 }
             }
-        }
-    }
-    // Each wave: nprobe rounds of extract-min over its lanes' list heads.
-    for (int r = 0; r < nprobe; r++) {
-        uint64_t k = bk[0];
-        int32_t i = bi[0];
-        wave_min(k, i);
-        if (bi[0] == i && bk[0] == k && k != KNONE) {
-#pragma unroll
-            for (int j = 0; j < PROBE_MAX - 1; j++) {
-                bk[j] = bk[j + 1];
-                bi[j] = bi[j + 1];
+            const int nb = s_nb;
+            if (nb == nprobe) t = min(t, (uint32_t)(s_bk[nprobe - 1] >> 32));
+            if (lane == 0) {
+                s_tau = t;
+                s_cnt = nb;
             }
-            bk[PROBE_MAX - 1] = KNONE;
-            bi[PROBE_MAX - 1] = INONE;
+            if (lane < nb) {  // the running top nprobe are candidates too
+                s_ck[lane] = s_bk[lane];
+                s_ci[lane] = s_bi[lane];
+            }
         }
-        if (lane == 0) {
-            s_k[w][r] = k;
-            s_i[w][r] = i;
+        __syncthreads();
+        const uint32_t tau = s_tau;
+        int npass = 0;
+#pragma unroll
+        for (int j = 0; j < SEL_J; j++) npass += __popcll(__ballot((uint32_t)(key[j] >> 32) <= tau && key[j] != KNONE));
+        int off = 0;
+        if (lane == 0 && npass) off = atomicAdd(&s_cnt, npass);
+        off = __shfl(off, 0, 64);
+#pragma unroll
+        for (int j = 0; j < SEL_J; j++) {
+            const bool pass = (uint32_t)(key[j] >> 32) <= tau && key[j] != KNONE;
+            const uint64_t bal = __ballot(pass);
+            const int pos = off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+            if (pass && pos < CAND) {
+                s_ck[pos] = key[j];
+                s_ci[pos] = base + j * SEL_T + tid;
+            }
+            off += __popcll(bal);
+        }
+        __syncthreads();
+        if (w == 0) {
+            const int cnt = s_cnt;
+            int nb = 0;
+            if (cnt <= 64) {
+                uint64_t k = lane < cnt ? s_ck[lane] : KNONE;
+                int32_t i = lane < cnt ? s_ci[lane] : INONE;
+                wave_sort_pair(k, i, lane);
+                nb = min(cnt, nprobe);
+                if (lane < nb) {
+                    s_bk[lane] = k;
+                    s_bi[lane] = i;
+                }
+            } else {
+                // nprobe successive minima strictly above the last one taken
+                // (the pairs are distinct): over the buffer, or, if it
+                // overflowed, over the round's cells and the running top.
+                const bool over = cnt > CAND;
+                const int nbo = s_nb;
+                const uint64_t tk = lane < nbo ? s_bk[lane] : KNONE;  // the running top, read before it is replaced
+                const int32_t ti = lane < nbo ? s_bi[lane] : INONE;
+                uint64_t lk = 0, rk = KNONE;
+                int32_t li = -1, ri = INONE;
+                const int end = min(nlist - base, SEL_ROUND);
+                for (int r = 0; r < nprobe; r++) {
+                    uint64_t bk = KNONE;
+                    int32_t bi = INONE;
+                    if (!over) {
+                        for (int e = lane; e < cnt; e += 64) {
+                            const uint64_t k = s_ck[e];
+                            const int32_t i = s_ci[e];
+                            if (lt(lk, li, k, i) && lt(k, i, bk, bi)) {
+                                bk = k;
+                                bi = i;
+                            }
+                        }
+                    } else {
+                        for (int e = lane; e < end; e += 64) {
+                            const uint64_t k = dkey(row[base + e]);
+                            const int32_t i = base + e;
+                            if (lt(lk, li, k, i) && lt(k, i, bk, bi)) {
+                                bk = k;
+                                bi = i;
+                            }
+                        }
+                        if (lt(lk, li, tk, ti) && lt(tk, ti, bk, bi)) {
+                            bk = tk;
+                            bi = ti;
+                        }
+                    }
+                    wave_min(bk, bi);
+                    if (bk == KNONE && bi == INONE) break;
+                    if (lane == r) {
+                        rk = bk;
+                        ri = bi;
+                    }
+                    lk = bk;
+                    li = bi;
+                    nb = r + 1;
+                }
+                if (lane < nb) {
+                    s_bk[lane] = rk;
+                    s_bi[lane] = ri;
+                }
+            }
+            if (lane == 0) s_nb = nb;
         }
     }
     __syncthreads();
-    if (w != 0) return;
-    // Wave 0: the 4 x nprobe (<= 64) wave results, one per lane, merged the same way.
-    uint64_t k = KNONE;
-    int32_t i = INONE;
-    if (lane < 4 * nprobe) {
-        k = s_k[lane / nprobe][lane % nprobe];
-        i = s_i[lane / nprobe][lane % nprobe];
-    }
-    for (int r = 0; r < nprobe; r++) {
-        uint64_t km = k;
-        int32_t im = i;
-        wave_min(km, im);
-        if (i == im && k == km) {
-            k = KNONE;
-            i = INONE;
-        }
-        if (lane == 0) probes[q * nprobe + r] = im == INONE ? -1 : im;
-    }
+    if (tid < nprobe) probes[q * nprobe + tid] = tid < s_nb ? s_bi[tid] : -1;
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -361,7 +481,7 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
         hipLaunchKernelGGL(k_probe_dots, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, qdig, qex, (int32_t)nqc,
                            digits, cexp, cnorm, (int32_t)nlist, (int32_t)per, dd);
         ST_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_probe_select, dim3((unsigned)nqc), dim3(256), 0, s, dd, (int32_t)nlist, (int32_t)nprobe,
+        hipLaunchKernelGGL(k_probe_select, dim3((unsigned)nqc), dim3(SEL_T), 0, s, dd, (int32_t)nlist, (int32_t)nprobe,
                            probes + q0 * nprobe);
         ST_LAUNCH_CHECK();
     }

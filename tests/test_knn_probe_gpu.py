@@ -103,3 +103,30 @@ def test_search_ivf_by_nprobe_end_to_end(dev):
     widx, wdist = oracle.knn_search(store.codes.cpu().numpy(), store.scales.cpu().numpy(), cell_start, queries, probes)
     np.testing.assert_array_equal(idx.cpu().numpy(), widx)
     np.testing.assert_array_equal(dist.cpu().numpy(), wdist)
+
+
+@pytest.mark.parametrize("case", ["all_equal", "many_equal_nearest", "near_equal_nearest", "one_cell_last_round"])
+def test_probe_selection_under_ties_and_round_edges(dev, case):
+    # Equal or near-equal distances fill the selection's candidate buffer past one
+    # wave (many_equal, near_equal) or past its capacity (all_equal: 3000 candidates);
+    # 12289 cells leave one cell for the second round of 12288.
+    rng = np.random.default_rng(34)
+    nlist = 12289 if case == "one_cell_last_round" else 3000
+    cent = rng.standard_normal((nlist, D)).astype(np.float32)
+    queries = rng.standard_normal((5, D)).astype(np.float32)
+    if case == "all_equal":
+        cent[:] = cent[0]
+    elif case in ("many_equal_nearest", "near_equal_nearest"):
+        idx = rng.choice(nlist, 300, replace=False)
+        cent[idx] = queries[0]
+        if case == "near_equal_nearest":
+            cent[idx] += np.float32(1e-4) * rng.standard_normal((300, D)).astype(np.float32)
+    else:
+        cent[12288] = queries[1]
+    for nprobe in (1, 8, 16):
+        _, got = run_probe(dev, cent, queries, nprobe)
+        np.testing.assert_array_equal(got, oracle.knn_probe(cent, queries, nprobe))
+    if case == "all_equal":
+        assert list(got[0]) == list(range(16))
+    if case == "one_cell_last_round":
+        assert got[1, 0] == 12288
