@@ -329,6 +329,35 @@ def bench_attention(dev, stream, steps, warmup, use_f16):
                 tflops=round(flops / graph_ms / 1e9, 3))
 
 
+def bench_attention_fused(dev, stream, steps, warmup):
+    """The same attention step as two fused launches (k_attn_fwd, k_attn_bwd): S and P never leave the chip."""
+    import torch
+    import oracle
+    from scratchtape_amd import attention
+    b, h, t, hd = 32, 4, 128, 64
+    d = h * hd
+    rng = oracle.Rng(17)
+    qkv = torch.from_numpy(oracle.round_f16(rng.gaussian(b * t * 3 * d))).to(dev)
+    dctx = torch.from_numpy(rng.gaussian(b * t * d)).to(dev)
+    buf = attention.FusedBuffers.empty(b, h, t, hd, dev)
+    fwd = lambda: attention.fused_forward(qkv, buf, b, h, t, hd)
+    bwd = lambda: attention.fused_backward(qkv, dctx, buf, b, h, t, hd)
+    step = lambda: attention.fused_step(qkv, dctx, buf, b, h, t, hd)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        eager_ms = time_events(step, steps, stream)
+        fwd_ms = time_events(fwd, steps, stream)
+        bwd_ms = time_events(bwd, steps, stream)
+        graph_ms, _ = time_graph(step, steps, warmup, stream)
+    flops = 6 * b * h * 2 * t * t * hd  # the six products of the unfused step, for comparison
+    # Algorithmic bytes: qkv read by both passes, dctx, ctx written then read, lse, dqkv written.
+    nbytes = 4 * (2 * b * t * 3 * d + b * t * d + 2 * b * t * d + 2 * b * h * t + b * t * 3 * d)
+    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_ms=round(graph_ms, 5), fwd_ms=round(fwd_ms, 5),
+                bwd_ms=round(bwd_ms, 5), tflops=round(flops / graph_ms / 1e9, 3),
+                roofline=roofline("k_attn_fwd + k_attn_bwd (fused f16 attention step)", flops, nbytes, graph_ms))
+
+
 def cpu_attention_baseline(reps=20):
     import oracle
     b, h, t, hd = 32, 4, 128, 64
@@ -568,6 +597,7 @@ def main():
         log("[bench] C4 attention")
         extra["c4_attention_f16"] = bench_attention(dev, stream, args.steps, args.warmup, True)
         extra["c4_attention_f32"] = bench_attention(dev, stream, args.steps, args.warmup, False)
+        extra["c4_attention_fused_f16"] = bench_attention_fused(dev, stream, args.steps, args.warmup)
         cpu = None
         if not args.no_cpu:
             log("[bench] CPU baselines (oracle, 1 thread)")

@@ -142,6 +142,28 @@ st_status st_softmax(const float *x, float *y, int64_t rows, int64_t n, int64_t 
 st_status st_softmax_backward(const float *dy, const float *y, float *dx, int64_t rows, int64_t n,
                               float scale, st_stream stream);
 
+/* ---- Fused causal attention ---------------------------------------------
+ * The attention of the device tape (tape.rs:73-112; gpu_step/tape.rs:196-212,
+ * 349-372: S = Q K^T, P = softmax(scale S) causal (rows.rs:101-112), O = P V
+ * and their backward) in two launches that never write S or P.  Q, K, V are
+ * the head-h column blocks [h hd, (h+1) hd) of the thirds of the fused QKV
+ * buffer qkv [b t, 3 D] (D = h_count hd, window-major rows); ctx [b t, D] is O
+ * in the merged layout; lse [b h_count t] the rows' log-sum-exp (max + log
+ * sum, softmax1's phantom term included when one != 0), which the backward
+ * uses to recompute P.  Operands are rounded to f16 (RNE) for f16 x f16 -> f32
+ * matrix cores, as the f16 GEMM route rounds.  hd == 64, t a multiple of 32 in
+ * 32..=256, 16-byte aligned buffers. */
+st_status st_attention_fused_fwd(const float *qkv, float *ctx, float *lse, int64_t b, int64_t h,
+                                 int64_t t, int64_t hd, float scale, int32_t one, st_stream stream);
+
+/* Backward of st_attention_fused_fwd for the upstream gradient dctx [b t, D]:
+ * writes dQ, dK, dV into the three blocks of dqkv [b t, 3 D] (every element;
+ * rows.rs:114-123's dS = scale P (dP - rowsum(dP o P)), with rowsum(dP o P)
+ * taken as rowsum(dO o O)). */
+st_status st_attention_fused_bwd(const float *qkv, const float *ctx, const float *dctx,
+                                 const float *lse, float *dqkv, int64_t b, int64_t h, int64_t t,
+                                 int64_t hd, float scale, st_stream stream);
+
 /* ---- 2-bit kNN memory ---------------------------------------------------- */
 
 /* gpu_step/knn.rs:190-225 `tile_of` (bits = 2) on the device: keys [n, d]

@@ -100,7 +100,7 @@ def lib():
         ]
         L.orc_softmax.argtypes = [_f32p, _f32p, _i64, _i64, _i64, ctypes.c_float, _i32, _i32]
         L.orc_softmax_backward.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_float]
-        L.orc_attention_fwd_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_float,
+        L.orc_attention_fwd_bwd.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_float, _i32,
                                             _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
         L.orc_quantize_2bit.argtypes = [_f32p, _i64, _i64, _u8p, _f32p, ctypes.c_void_p]
         L.orc_knn_prep_query.argtypes = [_f32p, _i64, _i16p, ctypes.POINTER(QPrep)]
@@ -225,13 +225,13 @@ def softmax_backward(dy: np.ndarray, y: np.ndarray, rows: int, n: int, scale: fl
     return dx
 
 
-def attention_fwd_bwd(q, k, v, dout, chunks, t, hd, scale):
-    """Per-chunk CPU attention forward + backward (tape.rs:73-112): returns P, O, dQ, dK, dV."""
+def attention_fwd_bwd(q, k, v, dout, chunks, t, hd, scale, one=False):
+    """Per-chunk CPU attention forward + backward (tape.rs:73-112): returns P, O, dQ, dK, dV (one: softmax1)."""
     arrs = [np.ascontiguousarray(x, np.float32).reshape(-1) for x in (q, k, v, dout)]
     p = np.empty(chunks * t * t, np.float32)
     o, dq, dk, dv = (np.empty(chunks * t * hd, np.float32) for _ in range(4))
     scratch = np.empty(4 * t * t + 3 * t * hd, np.float32)
-    lib().orc_attention_fwd_bwd(*arrs, chunks, t, hd, scale, p, o, dq, dk, dv, scratch)
+    lib().orc_attention_fwd_bwd(*arrs, chunks, t, hd, scale, int(one), p, o, dq, dk, dv, scratch)
     return p, o, dq, dk, dv
 
 

@@ -264,13 +264,14 @@ void orc_softmax_backward(const float *dy, const float *y, float *dx, int64_t ro
 /* Batched causal attention on the CPU tape path: batched_matmul_forward /   */
 /* backward (tape.rs:73-112) over per-chunk NdArray::matmul with explicit    */
 /* transposes, plus the causal softmax (nn.rs:396-407 mask, tape.rs:385-391).*/
-/* Q, K, V, dO are [chunks*t, hd] stacked chunk-major.  Outputs P [chunks*t, */
-/* t], O [chunks*t, hd] and dQ, dK, dV.  scratch must hold 4*t*t + 3*t*hd    */
-/* floats.  This is the CPU baseline of the attention configuration.          */
+/* Q, K, V, dO are [chunks*t, hd] stacked chunk-major; one: softmax1.        */
+/* Outputs P [chunks*t, t], O [chunks*t, hd] and dQ, dK, dV.  scratch must   */
+/* hold 4*t*t + 3*t*hd floats.  This is the CPU baseline of the attention    */
+/* configuration.                                                            */
 /* ------------------------------------------------------------------------ */
 void orc_attention_fwd_bwd(const float *q, const float *kk, const float *v, const float *dout,
-                           int64_t chunks, int64_t t, int64_t hd, float scale, float *p, float *o,
-                           float *dq, float *dk, float *dv, float *scratch) {
+                           int64_t chunks, int64_t t, int64_t hd, float scale, int32_t one, float *p,
+                           float *o, float *dq, float *dk, float *dv, float *scratch) {
     float *s = scratch;              /* [t, t] */
     float *kt = s + t * t;           /* [hd, t] */
     float *dp = kt + t * hd;         /* [t, t] */
@@ -285,7 +286,7 @@ void orc_attention_fwd_bwd(const float *q, const float *kk, const float *v, cons
         /* S = Q K^T (batched_matmul_forward, transpose_b) */
         orc_transpose(kc, kt, t, hd);
         orc_matmul(qc, kt, s, t, hd, t);
-        orc_softmax(s, pc, t, t, t, scale, 1, 0);
+        orc_softmax(s, pc, t, t, t, scale, 1, one);
         /* O = P V */
         orc_matmul(pc, vc, oc, t, t, hd);
         /* backward of O = P V: dP = dO V^T, dV = P^T dO */

@@ -7,6 +7,12 @@ probabilities P are stacked [B*H*T, T], the context is written into the merged
 [B*T, D] layout.  Every product goes through the GEMM of this package and the
 softmax through its row kernels; `use_f16` picks the f16-in/f32-acc route for
 the six products (the reference keeps them f32: matmul.rs:90-95).
+
+`fused_forward` / `fused_backward` compute the same attention in two launches
+that never write S or P (the reference's next step, docs/tiers_design.md:891-893):
+the forward keeps each row's log-sum-exp, from which the backward recomputes P.
+They run the f16-in/f32-acc route for head_dim 64 and sequence lengths that are
+multiples of 32 up to 256.
 """
 from __future__ import annotations
 
@@ -15,8 +21,8 @@ from typing import Optional
 
 import torch
 
-from . import rows
-from .matmul import Epilogue, MatRef, matmul_with
+from . import _lib, rows
+from .matmul import Epilogue, MatRef, _stream, matmul_with
 
 
 @dataclass
@@ -74,3 +80,42 @@ def step(qkv: torch.Tensor, dctx: torch.Tensor, buf: AttnBuffers, b: int, h: int
          use_f16: bool, stream: Optional[object] = None) -> None:
     forward(qkv, buf, b, h, t, hd, use_f16, stream)
     backward(qkv, dctx, buf, b, h, t, hd, use_f16, stream)
+
+
+@dataclass
+class FusedBuffers:
+    ctx: torch.Tensor   # [B*T, D] context
+    lse: torch.Tensor   # [B*H*T] log-sum-exp of each score row (kept for the backward)
+    dqkv: torch.Tensor  # [B*T, 3D] gradient of the fused QKV buffer
+
+    @staticmethod
+    def empty(b: int, h: int, t: int, hd: int, device) -> "FusedBuffers":
+        d = h * hd
+        z = lambda n: torch.zeros(n, dtype=torch.float32, device=device)
+        return FusedBuffers(z(b * t * d), z(b * h * t), z(b * t * 3 * d))
+
+
+def _f32(t: torch.Tensor, what: str) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous float32 GPU tensor")
+    return t.data_ptr()
+
+
+def fused_forward(qkv: torch.Tensor, buf: FusedBuffers, b: int, h: int, t: int, hd: int, one: bool = False,
+                  stream=None) -> None:
+    """O = softmax(hd^-1/2 Q K^T, causal) V into buf.ctx, row log-sum-exp into buf.lse."""
+    _lib.call("st_attention_fused_fwd", _f32(qkv, "qkv"), _f32(buf.ctx, "ctx"), _f32(buf.lse, "lse"), b, h, t, hd,
+              hd ** -0.5, int(one), _stream(stream))
+
+
+def fused_backward(qkv: torch.Tensor, dctx: torch.Tensor, buf: FusedBuffers, b: int, h: int, t: int, hd: int,
+                   stream=None) -> None:
+    """dQ, dK, dV of the fused forward for the upstream gradient dctx, into buf.dqkv."""
+    _lib.call("st_attention_fused_bwd", _f32(qkv, "qkv"), _f32(buf.ctx, "ctx"), _f32(dctx, "dctx"),
+              _f32(buf.lse, "lse"), _f32(buf.dqkv, "dqkv"), b, h, t, hd, hd ** -0.5, _stream(stream))
+
+
+def fused_step(qkv: torch.Tensor, dctx: torch.Tensor, buf: FusedBuffers, b: int, h: int, t: int, hd: int,
+               one: bool = False, stream: Optional[object] = None) -> None:
+    fused_forward(qkv, buf, b, h, t, hd, one, stream)
+    fused_backward(qkv, dctx, buf, b, h, t, hd, stream)

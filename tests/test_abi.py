@@ -101,3 +101,14 @@ def test_probe_arguments_are_validated_like_the_reference_asserts():
         assert msg in L.st_last_error(), (args, L.st_last_error())
     assert L.st_knn_centroids_prep(fake, 64, 200, fake, fake, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_knn_centroids_prep(fake, 0, 256, fake, fake, fake, None) == _lib.ST_ERR_INVALID
+
+
+def test_fused_attention_arguments_are_validated():
+    L = scratchtape_amd.lib()
+    fake = 1 << 20
+    for (b, h, t, hd), msg in [((32, 4, 128, 32), b"head_dim 64"), ((32, 4, 100, 64), b"multiple of 32"),
+                               ((32, 4, 288, 64), b"multiple of 32"), ((0, 4, 128, 64), b"batch")]:
+        assert L.st_attention_fused_fwd(fake, fake, fake, b, h, t, hd, 0.125, 0, None) == _lib.ST_ERR_INVALID
+        assert msg in L.st_last_error()
+        assert L.st_attention_fused_bwd(fake, fake, fake, fake, fake, b, h, t, hd, 0.125, None) == _lib.ST_ERR_INVALID
+    assert L.st_attention_fused_fwd(None, fake, fake, 32, 4, 128, 64, 0.125, 0, None) == _lib.ST_ERR_INVALID

@@ -81,3 +81,60 @@ def test_softmax_kernels_match_oracle(dev, one, amp, n, t):
     yy = y.cpu().numpy().reshape(rows_, n)
     for r in range(rows_):
         assert np.all(yy[r, (r % t) + 1:] == 0.0)
+
+
+# --------------------------------------------------------------------------- fused attention
+
+
+def fused_case(dev, b, h, t, one, seed):
+    d = h * HD
+    rng = oracle.Rng(seed)
+    qkv = oracle.round_f16(rng.gaussian(b * t * 3 * d).reshape(b * t, 3 * d))  # f16 Q, K, V
+    dctx = rng.gaussian(b * t * d).reshape(b * t, d)
+    buf = attention.FusedBuffers.empty(b, h, t, HD, dev)
+    attention.fused_step(torch.from_numpy(qkv).to(dev).reshape(-1), torch.from_numpy(dctx).to(dev).reshape(-1), buf,
+                         b, h, t, HD, one)
+    torch.cuda.synchronize()
+    heads = lambda x, c0, cols: x.reshape(b, t, cols)[:, :, c0:c0 + d].reshape(b, t, h, HD).transpose(0, 2, 1, 3) \
+        .reshape(b * h, t, HD)
+    q, k, v, do = heads(qkv, 0, 3 * d), heads(qkv, d, 3 * d), heads(qkv, 2 * d, 3 * d), heads(dctx, 0, d)
+    _, o, dq, dk, dv = oracle.attention_fwd_bwd(q, k, v, do, b * h, t, HD, HD ** -0.5, one)
+    dqkv = buf.dqkv.cpu().numpy().reshape(b * t, 3 * d)
+    got = {"O": heads(buf.ctx.cpu().numpy().reshape(b * t, d), 0, d), "dQ": heads(dqkv, 0, 3 * d),
+           "dK": heads(dqkv, d, 3 * d), "dV": heads(dqkv, 2 * d, 3 * d)}
+    want = {"O": o, "dQ": dq, "dK": dk, "dV": dv}
+    for name in want:
+        e = rel_err(got[name].reshape(-1), want[name].reshape(-1))
+        assert e <= 2e-3, f"{name}: {e} (b {b} h {h} t {t} one {one})"
+    # The saved row statistic is log(sum(exp(scale S))) over the causal row (plus softmax1's phantom).
+    S = np.einsum("zic,zjc->zij", q.astype(np.float64), k.astype(np.float64)) * HD ** -0.5
+    S = np.where(np.tril(np.ones((t, t), bool))[None], S, -np.inf)
+    mx = S.max(-1)
+    if one:
+        mx = np.maximum(mx, 0.0)
+    lse = mx + np.log(np.exp(S - mx[..., None]).sum(-1) + (np.exp(-mx) if one else 0.0))
+    assert np.max(np.abs(buf.lse.cpu().numpy().reshape(b * h, t) - lse)) <= 2e-3 * max(1.0, np.max(np.abs(lse)))
+    return buf
+
+
+def test_fused_attention_at_the_configured_shape(dev):
+    fused_case(dev, B, H, T, False, 17)
+
+
+@pytest.mark.parametrize("b,h,t,one", [(2, 3, 32, False), (3, 1, 64, True), (2, 2, 96, False), (1, 2, 160, False),
+                                        (2, 1, 256, True), (1, 5, 128, True)])
+def test_fused_attention_shapes_and_softmax1(dev, b, h, t, one):
+    fused_case(dev, b, h, t, one, 100 + t)
+
+
+def test_fused_attention_agrees_with_the_unfused_f16_route(dev):
+    rng = oracle.Rng(23)
+    qkv = torch.from_numpy(oracle.round_f16(rng.gaussian(B * T * 3 * D))).to(dev)
+    dctx = torch.from_numpy(rng.gaussian(B * T * D)).to(dev)
+    ub = attention.AttnBuffers.empty(B, H, T, HD, dev)
+    attention.step(qkv, dctx, ub, B, H, T, HD, True)
+    fb = attention.FusedBuffers.empty(B, H, T, HD, dev)
+    attention.fused_step(qkv, dctx, fb, B, H, T, HD)
+    torch.cuda.synchronize()
+    assert rel_err(fb.ctx.cpu().numpy(), ub.ctx.cpu().numpy()) <= 2e-3
+    assert rel_err(fb.dqkv.cpu().numpy(), ub.dqkv.cpu().numpy()) <= 4e-3

@@ -277,17 +277,21 @@ def test_softmax_forward_and_backward(one, amp):
         assert abs(dx[r, c] - fd) <= 1e-4 * max(1.0, abs(fd))
 
 
-def test_attention_fwd_bwd_matches_float64_closed_form():
+@pytest.mark.parametrize("one", [False, True])
+def test_attention_fwd_bwd_matches_float64_closed_form(one):
     chunks, t, hd = 3, 32, 16
     scale = 1.0 / math.sqrt(hd)
     rng = np.random.default_rng(4)
     q, k, v, do = (rng.standard_normal((chunks, t, hd)).astype(np.float32) for _ in range(4))
-    p, o, dq, dk, dv = oracle.attention_fwd_bwd(q, k, v, do, chunks, t, hd, scale)
+    p, o, dq, dk, dv = oracle.attention_fwd_bwd(q, k, v, do, chunks, t, hd, scale, one)
     Q, K, V, dO = (x.astype(np.float64) for x in (q, k, v, do))
     S = np.einsum("zic,zjc->zij", Q, K) * scale
     S = np.where(np.tril(np.ones((t, t), bool))[None], S, -np.inf)
-    P = np.exp(S - S.max(-1, keepdims=True))
-    P /= P.sum(-1, keepdims=True)
+    mx = S.max(-1, keepdims=True)
+    if one:  # softmax1: a phantom logit 0 in every row
+        mx = np.maximum(mx, 0.0)
+    P = np.exp(S - mx)
+    P /= P.sum(-1, keepdims=True) + (np.exp(-mx) if one else 0.0)
     O = P @ V
     dP = dO @ V.transpose(0, 2, 1)
     dV = P.transpose(0, 2, 1) @ dO
