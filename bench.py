@@ -358,6 +358,39 @@ def bench_attention_fused(dev, stream, steps, warmup):
                 roofline=roofline("k_attn_fwd + k_attn_bwd (fused f16 attention step)", flops, nbytes, graph_ms))
 
 
+def bench_layer_norm(dev, stream, steps, warmup):
+    """LayerNorm forward + backward at the step shape (T = 4096 rows of d_model 256), one parameter set."""
+    import torch
+    import oracle
+    from scratchtape_amd import rows
+    n, d = T_TOKENS, 256
+    rng = oracle.Rng(29)
+    x = torch.from_numpy(rng.gaussian(n * d)).to(dev)
+    dy = torch.from_numpy(rng.gaussian(n * d)).to(dev)
+    params = torch.from_numpy(np.concatenate([1.0 + 0.1 * rng.gaussian(d), 0.1 * rng.gaussian(d)]).astype(np.float32)).to(dev)
+    grads = torch.zeros(2 * d, device=dev)
+    dx = torch.empty(n * d, device=dev)
+    box = {}
+
+    def fwd():
+        box["f"] = rows.layer_norm(x, n, d, params, 0, 1e-5)
+
+    def step():
+        fwd()
+        rows.layer_norm_backward(dy, x, box["f"], n, d, params, grads, 0, dx, False)
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        fwd_ms = time_events(fwd, steps, stream)
+        graph_ms, _ = time_graph(step, steps, warmup, stream)
+    # Algorithmic bytes: x read and y written (forward); dy and x read, dx written (backward); mean, rstd.
+    nbytes = 4 * (5 * n * d + 4 * n)
+    return dict(rows=n, d=d, fwd_ms=round(fwd_ms, 5), graph_ms=round(graph_ms, 5),
+                roofline=roofline("k_ln_fwd + k_ln_bwd_dx + k_ln_bwd_part + k_ln_bwd_sum", 10 * n * d, nbytes,
+                                  graph_ms, route="f32"))
+
+
 def cpu_attention_baseline(reps=20):
     import oracle
     b, h, t, hd = 32, 4, 128, 64
@@ -598,6 +631,7 @@ def main():
         extra["c4_attention_f16"] = bench_attention(dev, stream, args.steps, args.warmup, True)
         extra["c4_attention_f32"] = bench_attention(dev, stream, args.steps, args.warmup, False)
         extra["c4_attention_fused_f16"] = bench_attention_fused(dev, stream, args.steps, args.warmup)
+        extra["c3_layer_norm"] = bench_layer_norm(dev, stream, args.steps, args.warmup)
         cpu = None
         if not args.no_cpu:
             log("[bench] CPU baselines (oracle, 1 thread)")

@@ -142,6 +142,27 @@ st_status st_softmax(const float *x, float *y, int64_t rows, int64_t n, int64_t 
 st_status st_softmax_backward(const float *dy, const float *y, float *dx, int64_t rows, int64_t n,
                               float scale, st_stream stream);
 
+/* gpu_step/rows.rs:65 `layer_norm` (k_ln_fwd rows.rs:177-207; nn.rs:306-321):
+ * y = (x - mean) / sqrt(var + eps) * gamma + beta per row of x [rows, d]
+ * (biased variance); mean [rows] and rstd [rows] = 1 / sqrt(var + eps) are
+ * kept for the backward.  gamma / beta are params[off + m stride + j] and
+ * + d for the rows of model m (`Models`: rows split evenly over `models`
+ * parameter sets `model_stride` floats apart; models = 1: stride unused). */
+st_status st_layer_norm(const float *x, int64_t rows, int64_t d, const float *params, int64_t off,
+                        float eps, int64_t models, int64_t model_stride, float *y, float *mean,
+                        float *rstd, st_stream stream);
+
+/* gpu_step/rows.rs:90 `layer_norm_backward` (k_ln_bwd_dx, k_ln_bwd_params
+ * rows.rs:209-293): dx (+)= rstd (g - mean(g) - xhat mean(g xhat)), g = dy
+ * gamma; grads[off + m stride + j] += sum of dy xhat over model m's rows,
+ * grads[... + d + j] += sum of dy (always accumulated, in a fixed order).
+ * Uses the library's row scratch arena (column partials): serialise on one
+ * stream per device. */
+st_status st_layer_norm_backward(const float *dy, const float *x, const float *mean,
+                                 const float *rstd, int64_t rows, int64_t d, const float *params,
+                                 float *grads, int64_t off, float *dx, int32_t accumulate,
+                                 int64_t models, int64_t model_stride, st_stream stream);
+
 /* ---- Fused causal attention ---------------------------------------------
  * The attention of the device tape (tape.rs:73-112; gpu_step/tape.rs:196-212,
  * 349-372: S = Q K^T, P = softmax(scale S) causal (rows.rs:101-112), O = P V

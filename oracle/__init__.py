@@ -21,6 +21,9 @@ transpose              src/tensor.rs:278-287                      involution, nu
 round_f16              half 2.7.1 from_f32 (RNE)                  IEEE-754 tie/overflow/subnormal KATs; numpy float16
 gemm (MatRef/Epilogue)  gpu_step/matmul.rs:26-79, 888-937         integer-valued exactness vs numpy int64 per epilogue
                                                                    term; head views vs explicit split_heads slicing
+layer_norm / backward  nn.rs:306-321, gpu_step/rows.rs:60-99,     float64 closed form; mean 0 / variance 1 of the
+                       177-293                                    normalised rows; finite-difference dx; dgamma/dbeta
+                                                                   as column sums; per-model parameter sets
 softmax / backward     gpu_step/rows.rs:101-123, 295-357          float64 softmax; rows sum to 1; masked entries exactly
                                                                    0; finite-difference gradient; softmax1 phantom term
 attention_fwd_bwd      src/tape.rs:73-112 (+ causal mask)         float64 closed-form attention forward and gradients
@@ -107,6 +110,9 @@ def lib():
         L.orc_knn_dists.argtypes = [_u8p, _f32p, _i64, _i64, _i64, _i16p, ctypes.POINTER(QPrep), _f32p]
         L.orc_knn_search.argtypes = [_u8p, _f32p, _i64p, _f32p, _i32p, _i64, _i64, _i64, _i64, _i64p, _f32p]
         L.orc_knn_ref_f16_dist.argtypes = [_u8p, ctypes.c_float, ctypes.c_float, _f32p, _i64]
+        L.orc_layer_norm.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_float, _i64, _i64, _f32p, _f32p, _f32p]
+        L.orc_layer_norm_backward.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p, _i32,
+                                              _i64, _i64]
         L.orc_knn_centroid_prep.argtypes = [_f32p, _i64, _i64, _i16p, _i32p, _f64p]
         L.orc_knn_probe.argtypes = [_i16p, _i32p, _f64p, _i64, _f32p, _i64, _i64, _i64, _i32p]
         L.orc_knn_ref_f16_dist.restype = ctypes.c_float
@@ -233,6 +239,29 @@ def attention_fwd_bwd(q, k, v, dout, chunks, t, hd, scale, one=False):
     scratch = np.empty(4 * t * t + 3 * t * hd, np.float32)
     lib().orc_attention_fwd_bwd(*arrs, chunks, t, hd, scale, int(one), p, o, dq, dk, dv, scratch)
     return p, o, dq, dk, dv
+
+
+def layer_norm(x, rows, d, params, off, eps=1e-5, rows_pm=None, stride=0):
+    """LayerNorm forward (nn.rs:306-321): returns (y, mean, rstd); rows_pm rows per parameter set."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    params = np.ascontiguousarray(params, np.float32)
+    y = np.empty(rows * d, np.float32)
+    mean, rstd = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    lib().orc_layer_norm(x, rows, d, params, off, eps, rows_pm or rows, stride, y, mean, rstd)
+    return y, mean, rstd
+
+
+def layer_norm_backward(dy, x, mean, rstd, rows, d, params, grads, off, dx=None, accumulate=False, rows_pm=None,
+                        stride=0):
+    """LayerNorm backward: returns dx; adds the gamma/beta gradients into grads (a float32 array, in place)."""
+    dy = np.ascontiguousarray(dy, np.float32).reshape(-1)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    dx = np.zeros(rows * d, np.float32) if dx is None else np.ascontiguousarray(dx, np.float32).copy()
+    assert grads.dtype == np.float32 and grads.flags.c_contiguous
+    lib().orc_layer_norm_backward(dy, x, np.ascontiguousarray(mean, np.float32), np.ascontiguousarray(rstd, np.float32),
+                                  rows, d, np.ascontiguousarray(params, np.float32), grads, off, dx, int(accumulate),
+                                  rows_pm or rows, stride)
+    return dx
 
 
 # --------------------------------------------------------------------------- kNN (knn.rs, ivf.rs)

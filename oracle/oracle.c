@@ -261,6 +261,77 @@ void orc_softmax_backward(const float *dy, const float *y, float *dx, int64_t ro
 }
 
 /* ------------------------------------------------------------------------ */
+/* LayerNorm (nn.rs:306-321 `LayerNorm::forward_shared`, composed on the CPU */
+/* tape; the device kernels rows.rs:65-99, 177-293).  Row r of x [rows, d]   */
+/* uses gamma/beta at params[off + (r / rows_pm) * stride + j] and + d      */
+/* (one parameter set per model of rows_pm rows).                            */
+/* ------------------------------------------------------------------------ */
+
+/* mean = (sum x) * (1/d); c = x - mean; var = (sum c^2) * (1/d) (biased);
+ * std = sqrt(var + eps); y = (c / std) * gamma + beta; rstd = 1 / std.
+ * Sums run in index order, every operation separately rounded, as the CPU
+ * tape's sum_last_axis / scale / sub / mul / add / sqrt / div do. */
+void orc_layer_norm(const float *x, int64_t rows, int64_t d, const float *params, int64_t off,
+                    float eps, int64_t rows_pm, int64_t stride, float *y, float *mean, float *rstd) {
+    const float inv_d = 1.0f / (float)d;
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * d;
+        const float *gm = params + off + (r / rows_pm) * stride, *bt = gm + d;
+        float s = 0.0f;
+        for (int64_t j = 0; j < d; j++) s += xr[j];
+        const float mu = s * inv_d;
+        float sq = 0.0f;
+        for (int64_t j = 0; j < d; j++) {
+            const float c = xr[j] - mu;
+            sq += c * c;
+        }
+        const float sd = sqrtf(sq * inv_d + eps);
+        for (int64_t j = 0; j < d; j++) y[r * d + j] = ((xr[j] - mu) / sd) * gm[j] + bt[j];
+        mean[r] = mu;
+        rstd[r] = 1.0f / sd;
+    }
+}
+
+/* The gradients of sum(dy * y): dx (+)= rstd (g - s1/d - xhat s2/d) with
+ * g = dy gamma, xhat = (x - mean) rstd, s1 = sum g, s2 = sum g xhat
+ * (rows.rs:221-267); grads[off + ...] += sum over the model's rows of dy xhat
+ * (gamma) and dy (beta) (rows.rs:269-291), rows summed in index order. */
+void orc_layer_norm_backward(const float *dy, const float *x, const float *mean, const float *rstd,
+                             int64_t rows, int64_t d, const float *params, float *grads, int64_t off,
+                             float *dx, int32_t accumulate, int64_t rows_pm, int64_t stride) {
+    const float inv_d = 1.0f / (float)d;
+    for (int64_t r = 0; r < rows; r++) {
+        const float *gm = params + off + (r / rows_pm) * stride;
+        const float mu = mean[r], rs = rstd[r];
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int64_t j = 0; j < d; j++) {
+            const float g = dy[r * d + j] * gm[j];
+            s1 += g;
+            s2 += g * ((x[r * d + j] - mu) * rs);
+        }
+        for (int64_t j = 0; j < d; j++) {
+            const float g = dy[r * d + j] * gm[j];
+            const float xh = (x[r * d + j] - mu) * rs;
+            float v = rs * (g - s1 * inv_d - xh * (s2 * inv_d));
+            dx[r * d + j] = accumulate ? dx[r * d + j] + v : v;
+        }
+    }
+    const int64_t models = (rows + rows_pm - 1) / rows_pm;
+    for (int64_t m = 0; m < models; m++) {
+        float *gg = grads + off + m * stride, *gb = gg + d;
+        for (int64_t j = 0; j < d; j++) {
+            float pg = 0.0f, pb = 0.0f;
+            for (int64_t r = m * rows_pm; r < (m + 1) * rows_pm && r < rows; r++) {
+                pg += dy[r * d + j] * ((x[r * d + j] - mean[r]) * rstd[r]);
+                pb += dy[r * d + j];
+            }
+            gg[j] += pg;
+            gb[j] += pb;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Batched causal attention on the CPU tape path: batched_matmul_forward /   */
 /* backward (tape.rs:73-112) over per-chunk NdArray::matmul with explicit    */
 /* transposes, plus the causal softmax (nn.rs:396-407 mask, tape.rs:385-391).*/

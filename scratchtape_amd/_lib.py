@@ -62,6 +62,8 @@ SIGNATURES = {
     "st_ndarray_matmul": [_vp, _vp, _vp, _i64, _i64, _i64],
     "st_softmax": [_vp, _vp, _i64, _i64, _i64, _f32, _i32, _i32, _vp],
     "st_softmax_backward": [_vp, _vp, _vp, _i64, _i64, _f32, _vp],
+    "st_layer_norm": [_vp, _i64, _i64, _vp, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _vp],
+    "st_layer_norm_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i64, _i64, _vp],
     "st_attention_fused_fwd": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "st_attention_fused_bwd": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "st_knn_quantize_2bit": [_vp, _i64, _i64, _vp, _vp, _vp],

@@ -24,7 +24,7 @@ void clear_error();
 // the new size; the old buffer is freed, which synchronises the device).
 // Never shrinks.  One arena per device and slot.  Returns nullptr and sets the
 // error on failure.
-enum ScratchSlot { SCRATCH_SPLITK = 0, SCRATCH_KNN = 1, SCRATCH_SLOTS = 2 };
+enum ScratchSlot { SCRATCH_SPLITK = 0, SCRATCH_KNN = 1, SCRATCH_ROWS = 2, SCRATCH_SLOTS = 3 };
 void *scratch(ScratchSlot slot, size_t bytes);
 
 // 1 when a gfx950 device is current; otherwise sets the error.

@@ -112,3 +112,14 @@ def test_fused_attention_arguments_are_validated():
         assert msg in L.st_last_error()
         assert L.st_attention_fused_bwd(fake, fake, fake, fake, fake, b, h, t, hd, 0.125, None) == _lib.ST_ERR_INVALID
     assert L.st_attention_fused_fwd(None, fake, fake, 32, 4, 128, 64, 0.125, 0, None) == _lib.ST_ERR_INVALID
+
+
+def test_layer_norm_arguments_are_validated():
+    L = scratchtape_amd.lib()
+    fake = 1 << 20
+    assert L.st_layer_norm(None, 4, 8, fake, 0, 1e-5, 1, 0, fake, fake, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_layer_norm(fake, 5, 8, fake, 0, 1e-5, 2, 16, fake, fake, fake, None) == _lib.ST_ERR_INVALID
+    assert b"split evenly" in L.st_last_error()
+    assert L.st_layer_norm_backward(fake, fake, fake, fake, 4, 8, fake, fake, 0, fake, 0, 2, 8, None) == \
+        _lib.ST_ERR_INVALID
+    assert b"overlap" in L.st_last_error()

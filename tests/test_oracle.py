@@ -233,6 +233,87 @@ def test_gemm_head_views_match_split_heads_slicing():
     np.testing.assert_array_equal(got, want)
 
 
+# --------------------------------------------------------------------------- LayerNorm (nn.rs, rows.rs)
+
+
+def _ln_params(d, off, models=1, stride=None):
+    stride = stride if stride is not None else 2 * d
+    flat = np.full(off + (models - 1) * stride + 2 * d + 1, 9.0, np.float32)
+    for m in range(models):
+        j = np.arange(d)
+        flat[off + m * stride: off + m * stride + d] = 1.0 + 0.1 * ((j * 7 + m) % 5)   # gamma (rows.rs:416-417)
+        flat[off + m * stride + d: off + m * stride + 2 * d] = 0.05 * ((j * 3 + m) % 4) - 0.1  # beta
+    return flat, stride
+
+
+@pytest.mark.parametrize("rows,d,off", [(37, 24, 5), (37, 200, 3), (203, 24, 5)])
+def test_layer_norm_matches_float64_closed_form(rows, d, off):
+    rng = oracle.Rng(7)
+    x = rng.gaussian(rows * d).reshape(rows, d)
+    r = rng.gaussian(rows * d).reshape(rows, d)
+    params, _ = _ln_params(d, off)
+    y, mean, rstd = oracle.layer_norm(x, rows, d, params, off, 1e-5)
+    X = x.astype(np.float64)
+    mu = X.mean(1, keepdims=True)
+    var = ((X - mu) ** 2).mean(1, keepdims=True)
+    xh = (X - mu) / np.sqrt(var + 1e-5)
+    gam, bet = params[off:off + d].astype(np.float64), params[off + d:off + 2 * d].astype(np.float64)
+    Y = xh * gam + bet
+    assert np.max(np.abs(y.reshape(rows, d) - Y)) <= 1e-5 * np.max(np.abs(Y))
+    assert np.allclose(mean, mu[:, 0], atol=1e-6) and np.allclose(rstd, 1 / np.sqrt(var[:, 0] + 1e-5), rtol=1e-5)
+    # Normalised rows (gamma 1, beta 0): mean 0, biased variance var / (var + eps).
+    ones = np.concatenate([np.ones(d, np.float32), np.zeros(d, np.float32)])
+    y1, _, _ = oracle.layer_norm(x, rows, d, ones, 0, 1e-5)
+    y1 = y1.reshape(rows, d).astype(np.float64)
+    assert np.max(np.abs(y1.mean(1))) < 1e-6 and np.allclose(y1.var(1), (var / (var + 1e-5))[:, 0], rtol=1e-5)
+    # Backward of sum(r * y): dx against float64 closed form and finite differences, dgamma / dbeta as column sums.
+    grads = np.full(params.size, 0.5, np.float32)
+    dx = oracle.layer_norm_backward(r, x, mean, rstd, rows, d, params, grads, off)
+    R = r.astype(np.float64)
+    g = R * gam
+    DX = (g - g.mean(1, keepdims=True) - xh * (g * xh).mean(1, keepdims=True)) / np.sqrt(var + 1e-5)
+    assert np.max(np.abs(dx.reshape(rows, d) - DX)) <= 1e-4 * np.max(np.abs(DX))
+    assert np.allclose(grads[off:off + d], 0.5 + (R * xh).sum(0), rtol=1e-4, atol=1e-4)
+    assert np.allclose(grads[off + d:off + 2 * d], 0.5 + R.sum(0), rtol=1e-4, atol=1e-4)
+    assert np.all(grads[:off] == 0.5) and np.all(grads[off + 2 * d:] == 0.5)
+    def loss(xx):
+        X2 = xx.astype(np.float64)
+        m2 = X2.mean(1, keepdims=True)
+        v2 = ((X2 - m2) ** 2).mean(1, keepdims=True)
+        return (R * (((X2 - m2) / np.sqrt(v2 + 1e-5)) * gam + bet)).sum()
+    for (i, j) in [(0, 0), (rows // 2, d - 1), (rows - 1, 3)]:
+        xp, xm = x.astype(np.float64).copy(), x.astype(np.float64).copy()
+        xp[i, j] += 1e-6
+        xm[i, j] -= 1e-6
+        fd = (loss(xp) - loss(xm)) / 2e-6
+        assert abs(dx.reshape(rows, d)[i, j] - fd) <= 1e-3 * max(1.0, abs(fd))
+    # Accumulate adds onto dx.
+    dx2 = oracle.layer_norm_backward(r, x, mean, rstd, rows, d, params, np.zeros_like(grads), off, dx=dx, accumulate=True)
+    assert np.allclose(dx2, 2 * dx, rtol=1e-6, atol=1e-7)
+
+
+def test_layer_norm_per_model_parameter_sets():
+    # Two models of 30 rows, parameter sets 3 d + 1 floats apart: each row uses its model's set, and
+    # each model's gradients land in its own set.
+    rows, d, off, k = 60, 16, 2, 2
+    params, stride = _ln_params(d, off, models=k, stride=3 * d + 1)
+    rng = oracle.Rng(9)
+    x, r = rng.gaussian(rows * d), rng.gaussian(rows * d)
+    y, mean, rstd = oracle.layer_norm(x, rows, d, params, off, 1e-5, rows_pm=30, stride=stride)
+    grads = np.zeros(params.size, np.float32)
+    dx = oracle.layer_norm_backward(r, x, mean, rstd, rows, d, params, grads, off, rows_pm=30, stride=stride)
+    for m in range(k):
+        sl = slice(m * 30 * d, (m + 1) * 30 * d)
+        p1 = params[off + m * stride: off + m * stride + 2 * d]
+        ym, _, _ = oracle.layer_norm(x[sl], 30, d, p1, 0, 1e-5)
+        np.testing.assert_array_equal(y[sl], ym)
+        g1 = np.zeros(2 * d, np.float32)
+        dxm = oracle.layer_norm_backward(r[sl], x[sl], mean[m * 30:(m + 1) * 30], rstd[m * 30:(m + 1) * 30], 30, d, p1,
+                                         g1, 0)
+        np.testing.assert_array_equal(dx[sl], dxm)
+        np.testing.assert_array_equal(grads[off + m * stride: off + m * stride + 2 * d], g1)
+
+
 # --------------------------------------------------------------------------- softmax (rows.rs)
 
 
