@@ -241,6 +241,19 @@ st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, const double *
                        const float *queries, int64_t nq, int64_t d, int64_t nprobe, int32_t *probes,
                        st_stream stream);
 
+/* gpu_step/knn.rs:295-331 `search_tagged` / `search_tail` (masked exact
+ * search; key predicate of k_thresh / k_topk knn.rs:604-618) on the 2-bit
+ * store of nkeys rows (KMAX <= nkeys < 2^31): query i scores the keys
+ * g < always and lohi[2i] <= g < lohi[2i+1] (ranges clipped to the store;
+ * lohi [nq, 2] int64 device) with the scoring and outputs of
+ * st_knn_search_ivf_2bit (k nearest by (distance, key index), global key
+ * rows, -1 / +inf padding).  The reference's from_key only skips tiles below
+ * the ranges; scanning the two segments does that by construction. */
+st_status st_knn_search_masked_2bit(const uint8_t *codes, const float *scales, int64_t nkeys,
+                                    const float *queries, const int64_t *lohi, int64_t always,
+                                    int64_t nq, int64_t d, int64_t k, int64_t *out_idx,
+                                    float *out_dist, st_stream stream);
+
 /* Benchmark support, no reference counterpart: fills rows [row0, row0 + n)
  * of a synthetic 2-bit store with keys drawn N(0,1) from a counter-based
  * generator (seed, global row, component) and quantised as

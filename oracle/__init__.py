@@ -34,6 +34,9 @@ knn_prep_query         build contract (int16 query)               exactness: Q*q
 knn_search             build contract (ivf.rs:235 distance,       int64 brute force + numpy float32 formula + lexsort;
                        ivf.rs:673-684 finalisation)               exact integer dot vs float64; fidelity to the
                                                                    reference's own f16 scoring within its 2e-3 tolerance
+knn_search_masked      knn.rs:295-331 search_tagged/search_tail,  the IVF brute force with the mask predicate; equality
+                       key predicate knn.rs:604-618               with knn_search when the range is one cell; always
+                                                                   prefix, empty and clipped ranges
 knn_centroid_prep      ivf.rs:62-69 Cent::new, with the scan's     exactness: C * 2^cexp reproduces the centroid as
                        int16 quantiser in place of f16 rounding  knn_prep_query does; cnorm = float64 |C 2^cexp|^2
 knn_probe              ivf.rs:128-161 k_probe over the dots of     float64 brute force of |q - c|^2 (ranking agrees
@@ -71,7 +74,7 @@ class _MatRef(ctypes.Structure):
 
 
 class QPrep(ctypes.Structure):
-    _fields_ = [("qs", ctypes.c_float), ("qn", ctypes.c_float), ("sq", _i32), ("pad", _i32)]
+    _fields_ = [("qs", ctypes.c_float), ("qn", ctypes.c_float), ("sq", _i32), ("qe", _i32)]
 
 
 def build() -> None:
@@ -109,6 +112,8 @@ def lib():
         L.orc_knn_prep_query.argtypes = [_f32p, _i64, _i16p, ctypes.POINTER(QPrep)]
         L.orc_knn_dists.argtypes = [_u8p, _f32p, _i64, _i64, _i64, _i16p, ctypes.POINTER(QPrep), _f32p]
         L.orc_knn_search.argtypes = [_u8p, _f32p, _i64p, _f32p, _i32p, _i64, _i64, _i64, _i64, _i64p, _f32p]
+        L.orc_knn_search_masked.argtypes = [_u8p, _f32p, _i64, _f32p, _i64p, _i64p, _i64, _i64, _i64, _i64, _i64p,
+                                             _f32p]
         L.orc_knn_ref_f16_dist.argtypes = [_u8p, ctypes.c_float, ctypes.c_float, _f32p, _i64]
         L.orc_layer_norm.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_float, _i64, _i64, _f32p, _f32p, _f32p]
         L.orc_layer_norm_backward.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p, _i32,
@@ -305,6 +310,19 @@ def knn_search(codes, scales, cell_start, queries, probes, k=128):
     idx = np.empty((nq, k), np.int64)
     dist = np.empty((nq, k), np.float32)
     lib().orc_knn_search(codes, scales, cell_start, queries.reshape(-1), probes, nq, nprobe, d, k, idx, dist)
+    return idx, dist
+
+
+def knn_search_masked(codes, scales, queries, lo, hi, always=0, k=128):
+    """Top-k by (dist, key index) over keys g < always or lo[i] <= g < hi[i] (knn.rs:295-331, 604-618)."""
+    codes = np.ascontiguousarray(codes, np.uint8).reshape(-1)
+    scales = np.ascontiguousarray(scales, np.float32)
+    queries = np.ascontiguousarray(queries, np.float32)
+    nq, d = queries.shape
+    idx = np.empty((nq, k), np.int64)
+    dist = np.empty((nq, k), np.float32)
+    lib().orc_knn_search_masked(codes, scales, scales.size, queries.reshape(-1), np.ascontiguousarray(lo, np.int64),
+                                np.ascontiguousarray(hi, np.int64), always, nq, d, k, idx.reshape(-1), dist.reshape(-1))
     return idx, dist
 
 

@@ -432,10 +432,10 @@ void orc_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t *codes, 
 /* ------------------------------------------------------------------------ */
 
 typedef struct {
-    float qs;     /* power-of-two query scale */
+    float qs;     /* power-of-two query scale 2^qe */
     float qn;     /* |q^|^2 */
     int32_t sq;   /* sum Q_i */
-    int32_t pad;
+    int32_t qe;   /* the scale's exponent */
 } orc_qprep;
 
 void orc_knn_prep_query(const float *q, int64_t d, int16_t *Q, orc_qprep *prep) {
@@ -444,16 +444,14 @@ void orc_knn_prep_query(const float *q, int64_t d, int16_t *Q, orc_qprep *prep) 
         float a = fabsf(q[i]);
         if (a > mx) mx = a;
     }
-    float qs = 1.0f;
-    if (mx > 0.0f) {
-        int e;
-        frexpf(mx, &e);
-        qs = ldexpf(1.0f, e - 14);
-    }
+    int e = 14; /* scale 2^0 for a zero vector */
+    if (mx > 0.0f) frexpf(mx, &e);
+    const float qs = ldexpf(1.0f, e - 14);
     int64_t sq2 = 0;
     int32_t sq = 0;
     for (int64_t i = 0; i < d; i++) {
-        float v = rintf(q[i] / qs);
+        /* q / 2^(e-14), exact (|result| < 2^14) even where 2^(e-14) is subnormal */
+        float v = rintf(ldexpf(q[i], 14 - e));
         if (v > 16383.0f) v = 16383.0f;
         if (v < -16384.0f) v = -16384.0f;
         int32_t x = (int32_t)v;
@@ -464,7 +462,7 @@ void orc_knn_prep_query(const float *q, int64_t d, int16_t *Q, orc_qprep *prep) 
     prep->qs = qs;
     prep->qn = (float)sq2 * (qs * qs);
     prep->sq = sq;
-    prep->pad = 0;
+    prep->qe = e - 14;
 }
 
 static inline float knn_dist(const uint8_t *code, float s, const int16_t *Q, float qs, int64_t d) {
@@ -574,6 +572,58 @@ void orc_knn_search(const uint8_t *codes, const float *scales, const int64_t *ce
     free(Q);
 }
 
+/* The masked exact search (knn.rs:295-331 search_tagged / search_tail, the
+ * key predicate of k_thresh / k_topk knn.rs:604-618): for query i, key g of
+ * the store [0, n) takes part iff g < always or lo[i] <= g < hi[i]; top-k by
+ * (dist, key index) over those keys, outputs as orc_knn_search. */
+void orc_knn_search_masked(const uint8_t *codes, const float *scales, int64_t n, const float *queries,
+                           const int64_t *lo, const int64_t *hi, int64_t always, int64_t nq, int64_t d,
+                           int64_t k, int64_t *out_idx, float *out_dist) {
+    int64_t kb = d / 4;
+    int16_t *Q = (int16_t *)malloc(sizeof(int16_t) * (size_t)d);
+    uint64_t *heap = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)k);
+    for (int64_t qi = 0; qi < nq; qi++) {
+        orc_qprep prep;
+        orc_knn_prep_query(queries + qi * d, d, Q, &prep);
+        int64_t size = 0;
+        for (int64_t g = 0; g < n; g++) {
+            if (!(g < always || (g >= lo[qi] && g < hi[qi]))) continue;
+            float dist = knn_dist(codes + g * kb, scales[g], Q, prep.qs, d);
+            uint64_t key = ((uint64_t)fkey(dist) << 32) | (uint64_t)(uint32_t)g;
+            if (size < k) {
+                int64_t i = size++;
+                while (i > 0) {
+                    int64_t par = (i - 1) / 2;
+                    if (heap[par] >= key) break;
+                    heap[i] = heap[par];
+                    i = par;
+                }
+                heap[i] = key;
+            } else if (key < heap[0]) {
+                heap[0] = key;
+                heap_sift_down(heap, size, 0);
+            }
+        }
+        qsort(heap, (size_t)size, sizeof(uint64_t), cmp_u64);
+        for (int64_t j = 0; j < k; j++) {
+            if (j < size) {
+                uint32_t fk = (uint32_t)(heap[j] >> 32);
+                uint32_t bits = (fk & 0x80000000u) ? (fk & 0x7fffffffu) : ~fk;
+                float dist;
+                memcpy(&dist, &bits, 4);
+                float v = prep.qn + dist;
+                out_dist[qi * k + j] = v > 0.0f ? v : 0.0f;
+                out_idx[qi * k + j] = (int64_t)(uint32_t)heap[j];
+            } else {
+                out_dist[qi * k + j] = INFINITY;
+                out_idx[qi * k + j] = -1;
+            }
+        }
+    }
+    free(heap);
+    free(Q);
+}
+
 /* The reference's own f16 scoring of one key, for fidelity checks: q and the
  * dequantised key both rounded to f16 (ivf.rs:470, k_dots_group ivf.rs:295-300),
  * dot summed in f32 in index order; returns |q^|^2 + norm - 2 q^.k^ with the
@@ -606,7 +656,7 @@ void orc_knn_centroid_prep(const float *cent, int64_t nlist, int64_t d, int16_t 
         orc_knn_prep_query(cent + c * d, d, C + c * d, &p);
         int64_t s2 = 0;
         for (int64_t i = 0; i < d; i++) s2 += (int64_t)C[c * d + i] * C[c * d + i];
-        cexp[c] = ilogbf(p.qs);
+        cexp[c] = p.qe;
         cnorm[c] = ldexp((double)s2, 2 * cexp[c]);
     }
 }
@@ -624,7 +674,7 @@ void orc_knn_probe(const int16_t *C, const int32_t *cexp, const double *cnorm, i
     for (int64_t qi = 0; qi < nq; qi++) {
         orc_qprep p;
         orc_knn_prep_query(queries + qi * d, d, Q, &p);
-        const int qe = ilogbf(p.qs);
+        const int qe = p.qe;
         int64_t size = 0;
         for (int64_t c = 0; c < nlist; c++) {
             int64_t dot = 0;

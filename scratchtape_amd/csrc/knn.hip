@@ -211,18 +211,15 @@ __device__ __forceinline__ QInfo quantize_query(const float *qrow, int lane, int
     const float4 v = reinterpret_cast<const float4 *>(qrow)[lane];
     const float x[4] = {v.x, v.y, v.z, v.w};
     const float mx = wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
-    float qs = 1.f, inv = 1.f;
-    if (mx > 0.f) {
-        int e;
-        frexpf(mx, &e);
-        qs = ldexpf(1.f, e - 14);
-        inv = ldexpf(1.f, 14 - e);
-    }
+    int e = 14;  // scale 2^0 for a zero query
+    if (mx > 0.f) frexpf(mx, &e);
+    const float qs = ldexpf(1.f, e - 14);
     int32_t sq = 0;
     double sq2 = 0.0;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int32_t Q = (int32_t)fminf(fmaxf(rintf(x[t] * inv), -16384.f), 16383.f);
+        // x / 2^(e-14), exact (|result| < 2^14) even where 2^(e-14) is subnormal
+        const int32_t Q = (int32_t)fminf(fmaxf(rintf(ldexpf(x[t], 14 - e)), -16384.f), 16383.f);
         sq += Q;
         sq2 += (double)Q * (double)Q;
         sQ[4 * lane + t] = (int16_t)Q;
@@ -396,12 +393,17 @@ __device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, in
     return k;
 }
 
-// grid: one workgroup of 1024 threads per query.
+// grid: one workgroup of 1024 threads per query.  IVF mode (MASKED false):
+// the query scans its probed cells (probes, cell_start).  MASKED: it scans
+// the keys g < always and lo <= g < hi of the store's nkeys (lohi [nq, 2]),
+// as two row segments; cell_start, probes, ncells and nprobe are unused.
+template <bool MASKED>
 __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const float *scales,
                                                 const int64_t *__restrict__ cell_start, int64_t ncells,
                                                 const float *__restrict__ queries, const int32_t *__restrict__ probes,
                                                 int32_t nq, int32_t nprobe, int32_t k, int64_t *__restrict__ out_idx,
-                                                float *__restrict__ out_dist) {
+                                                float *__restrict__ out_dist, const int64_t *__restrict__ lohi,
+                                                int64_t always, int64_t nkeys) {
     __shared__ uint64_t cand[SW * CAPW];  // per-wave candidate lists
     __shared__ uint64_t fin[SW * KMAX];   // the final gather
     __shared__ uint64_t s_tau;            // shared threshold (only decreases)
@@ -416,7 +418,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t q = blockIdx.x;
-    const int64_t total = (int64_t)nq * nprobe;
+    const int64_t total = MASKED ? 0 : (int64_t)nq * nprobe;
     const int32_t pv0 = tid < total ? probes[tid] : -1;
     const int32_t pv1 = tid + STH < total ? probes[tid + STH] : -1;
 
@@ -427,7 +429,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             s_qn = qi.qn;
             s_sq = qi.sq;
         }
-    } else if (wave == 1) {
+    } else if (wave == 1 && !MASKED) {
         // The probed cells and their row ranges (all loads in flight together);
         // an id outside [0, ncells) is recorded as -1 and skipped.
         if (lane < nprobe) {
@@ -456,7 +458,28 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             if (v == s_cell[jj]) atomicAdd(&s_share[jj], 1);
     }
     __syncthreads();
-    if (tid == 0) {
+    if (MASKED && tid == 0) {
+        // Segments [0, min(always, nkeys)) and [max(lo, always), min(hi, nkeys)).
+        const int64_t lo = lohi[2 * q], hi = lohi[2 * q + 1];
+        const int64_t a1 = always < nkeys ? always : nkeys;
+        const int64_t b0 = lo > always ? lo : always, b1 = hi < nkeys ? hi : nkeys;
+        int np = 0;
+        s_cpre[0] = 0;
+        if (a1 > 0) {
+            s_r0[np] = 0;
+            s_len[np] = (int32_t)a1;
+            s_cpre[np + 1] = (int32_t)((a1 + 63) / 64);
+            np++;
+        }
+        if (b1 > b0) {
+            s_r0[np] = b0;
+            s_len[np] = (int32_t)(b1 - b0);
+            s_cpre[np + 1] = s_cpre[np] + (int32_t)((b1 - b0 + 63) / 64);
+            np++;
+        }
+        s_np = np;
+        s_nrows = nkeys;
+    } else if (!MASKED && tid == 0) {
         // Cells scanned by several queries of the batch first (their bytes are
         // then read while still in the MALL), a repeated cell once, invalid ids
         // skipped; s_cpre counts 64-key chunks.
@@ -734,8 +757,35 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     if (nq > INT32_MAX / PROBE_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many queries for one call");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     const hipStream_t s = st::stream_of(stream);
-    hipLaunchKernelGGL(k_search, dim3((unsigned)nq), dim3(STH), 0, s, codes, scales, cell_start, ncells, queries,
-                       probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist);
+    hipLaunchKernelGGL(k_search<false>, dim3((unsigned)nq), dim3(STH), 0, s, codes, scales, cell_start, ncells, queries,
+                       probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist, nullptr, (int64_t)0,
+                       (int64_t)0);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}
+
+extern "C" st_status st_knn_search_masked_2bit(const uint8_t *codes, const float *scales, int64_t nkeys,
+                                               const float *queries, const int64_t *lohi, int64_t always,
+                                               int64_t nq, int64_t d, int64_t k, int64_t *out_idx, float *out_dist,
+                                               st_stream stream) {
+    st::clear_error();
+    if (!codes || !scales || !queries || !lohi || !out_idx || !out_dist)
+        return st::fail(ST_ERR_INVALID, "search_masked: NULL buffer");
+    if (d != D) return st::fail(ST_ERR_INVALID, "search_masked: the 2-bit scan is built for d == %d (got %lld)", D,
+                                (long long)d);
+    if (nkeys < KMAX) return st::fail(ST_ERR_INVALID, "need at least %d keys", KMAX);  // knn.rs:305
+    if (nkeys >= (1ll << 31)) return st::fail(ST_ERR_INVALID, "search_masked: the store must hold fewer than 2^31 keys");
+    if (nq < 0 || always < 0) return st::fail(ST_ERR_INVALID, "search_masked: bad nq or always");
+    if (k < 1 || k > KMAX) return st::fail(ST_ERR_INVALID, "search_masked: k must be in 1..=%d (got %lld)", KMAX,
+                                           (long long)k);
+    if ((reinterpret_cast<uintptr_t>(codes) & 15) != 0 || (reinterpret_cast<uintptr_t>(queries) & 15) != 0)
+        return st::fail(ST_ERR_INVALID, "search_masked: codes and queries must be 16-byte aligned");
+    if (nq == 0) return ST_OK;
+    if (nq > INT32_MAX) return st::fail(ST_ERR_INVALID, "search_masked: too many queries for one call");
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    hipLaunchKernelGGL(k_search<true>, dim3((unsigned)nq), dim3(STH), 0, st::stream_of(stream), codes, scales,
+                       nullptr, (int64_t)0, queries, nullptr, (int32_t)nq, 0, (int32_t)k, out_idx, out_dist, lohi,
+                       always, nkeys);
     ST_LAUNCH_CHECK();
     return ST_OK;
 }

@@ -12,6 +12,8 @@ Probe selection (ivf.rs:62-69 `Cent`, ivf.rs:128-161 `k_probe`, the probe stage
 of `search_ivf` ivf.rs:473-489) runs on the device too: `Centroids` holds the
 quantised centroids, and `search_ivf(queries, nprobe)` picks each query's
 nprobe nearest cells by the exact integer distance before scanning them.
+`search_masked` is the store's masked exact search (knn.rs:295-331): each query
+scores the keys of its own (lo, hi) range plus an always-visible prefix.
 """
 from __future__ import annotations
 
@@ -163,4 +165,24 @@ class KnnStore2bit:
                   self.max_cell, _dptr(queries, torch.float32, "queries"), _dptr(probes, torch.int32, "probes"),
                   nq, nprobe, d, k, _dptr(idx, torch.int64, "idx"), _dptr(dist, torch.float32, "dist"),
                   _stream(stream))
+        return idx, dist
+
+    def search_masked(self, queries: torch.Tensor, lohi: torch.Tensor, always: int = 0, k: int = KMAX,
+                      out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, stream=None):
+        """The k nearest among keys g < always or lo_i <= g < hi_i (knn.rs:295-331 search_tagged / search_tail):
+        (idx [nq, k] int64, dist [nq, k] float32).  lohi [nq, 2] int64 (device), one (lo, hi) range per query."""
+        nq, d = queries.shape
+        if d != self.d:
+            raise ValueError(f"queries have width {d}, the store {self.d}")
+        if lohi.shape != (nq, 2):
+            raise ValueError("one (lo, hi) range per query")
+        if out is None:
+            idx = torch.empty((nq, k), dtype=torch.int64, device=queries.device)
+            dist = torch.empty((nq, k), dtype=torch.float32, device=queries.device)
+        else:
+            idx, dist = out
+        _lib.call("st_knn_search_masked_2bit", _dptr(self.codes, torch.uint8, "codes"),
+                  _dptr(self.scales, torch.float32, "scales"), len(self), _dptr(queries, torch.float32, "queries"),
+                  _dptr(lohi, torch.int64, "lohi"), always, nq, d, k, _dptr(idx, torch.int64, "idx"),
+                  _dptr(dist, torch.float32, "dist"), _stream(stream))
         return idx, dist

@@ -123,3 +123,15 @@ def test_layer_norm_arguments_are_validated():
     assert L.st_layer_norm_backward(fake, fake, fake, fake, 4, 8, fake, fake, 0, fake, 0, 2, 8, None) == \
         _lib.ST_ERR_INVALID
     assert b"overlap" in L.st_last_error()
+
+
+def test_masked_search_arguments_are_validated():
+    L = scratchtape_amd.lib()
+    fake = 1 << 20
+    assert L.st_knn_search_masked_2bit(fake, fake, 100, fake, fake, 0, 4, 256, 128, fake, fake, None) == \
+        _lib.ST_ERR_INVALID
+    assert b"at least 128 keys" in L.st_last_error()
+    assert L.st_knn_search_masked_2bit(fake, fake, 1000, fake, fake, 0, 4, 128, 128, fake, fake, None) == \
+        _lib.ST_ERR_INVALID
+    assert L.st_knn_search_masked_2bit(fake, fake, 1000, fake, fake, 0, 4, 256, 129, fake, fake, None) == \
+        _lib.ST_ERR_INVALID

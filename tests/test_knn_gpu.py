@@ -171,3 +171,51 @@ def test_full_store_125m_keys(dev):
     assert np.all(np.any(cell_of[:, :, None] == probes[:, None, :], axis=2))
     del codes, scales, store
     torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------- masked exact search (knn.rs:295-331)
+
+
+@pytest.mark.parametrize("always,k", [(0, 128), (37, 128), (5000, 10), (20000, 128)])
+def test_masked_search_matches_oracle(dev, always, k):
+    rng = np.random.default_rng(51)
+    n, nq = 20000, 40
+    keys = rng.standard_normal((n, D)).astype(np.float32)
+    store = knn.KnnStore2bit.from_keys(torch.from_numpy(keys).to(dev), np.array([0, n], np.int64))
+    codes, scales = store.codes.cpu().numpy(), store.scales.cpu().numpy()
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    lo = rng.integers(0, n, nq)
+    hi = lo + rng.integers(0, 6000, nq)  # some past the store's end (clipped)
+    lo[0], hi[0] = 300, 300              # empty range: the always prefix only
+    lo[1], hi[1] = n - 5, n + 100        # 5 keys
+    lo[2], hi[2] = 0, n                  # everything
+    lo[3], hi[3] = 64, 128               # one aligned chunk
+    lo[4], hi[4] = 10, 5                 # inverted: empty
+    queries[5] *= np.float32(2.0 ** -130)  # a subnormal query (exact power-of-two quantisation)
+    lohi = torch.from_numpy(np.stack([lo, hi], 1).astype(np.int64)).to(dev)
+    idx, dist = store.search_masked(torch.from_numpy(queries).to(dev), lohi, always, k)
+    widx, wdist = oracle.knn_search_masked(codes, scales, queries, lo, hi, always, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), widx)
+    np.testing.assert_array_equal(dist.cpu().numpy(), wdist)
+
+
+def test_masked_search_over_a_window_of_the_full_store(dev):
+    # The 125M-key store's last 1M keys as the in-document window of 4 queries (search_tail's use).
+    n = 125_000_000
+    codes = torch.empty((n, D // 4), dtype=torch.uint8, device=dev)
+    scales = torch.empty(n, dtype=torch.float32, device=dev)
+    knn.synth_store_2bit(2024, 0, codes, scales)
+    store = knn.KnnStore2bit(codes, scales, np.array([0, n], np.int64))
+    rng = np.random.default_rng(52)
+    queries = rng.standard_normal((4, D)).astype(np.float32)
+    lo = np.array([n - 1_000_000, n - 700_000, n - 65, n - 1_000_000], np.int64)
+    hi = np.array([n, n - 300_000, n, n - 999_000], np.int64)
+    lohi = torch.from_numpy(np.stack([lo, hi], 1)).to(dev)
+    idx, dist = store.search_masked(torch.from_numpy(queries).to(dev), lohi, 0, 128)
+    w0 = int(lo.min())
+    sub_codes, sub_scales = codes[w0:].cpu().numpy(), scales[w0:].cpu().numpy()
+    widx, wdist = oracle.knn_search_masked(sub_codes, sub_scales, queries, lo - w0, hi - w0, 0, 128)
+    np.testing.assert_array_equal(idx.cpu().numpy(), np.where(widx >= 0, widx + w0, -1))
+    np.testing.assert_array_equal(dist.cpu().numpy(), wdist)
+    del codes, scales
+    torch.cuda.empty_cache()

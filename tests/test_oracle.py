@@ -505,6 +505,51 @@ def test_knn_search_equals_brute_force_and_handles_edges():
     assert np.all(idx[0][5:] == -1) and np.all(np.isinf(dist[0][5:]))
 
 
+def test_knn_masked_search_equals_brute_force_over_the_allowed_keys():
+    d, n, nq = 256, 3000, 12
+    rng = np.random.default_rng(41)
+    keys = rng.standard_normal((n, d)).astype(np.float32)
+    codes, scales = oracle.quantize_2bit(keys, d)
+    queries = rng.standard_normal((nq, d)).astype(np.float32)
+    lo = rng.integers(0, n, nq)
+    hi = np.minimum(lo + rng.integers(0, 900, nq), n + 50)  # some ranges run past the store (clipped)
+    lo[0], hi[0] = 100, 100        # empty range: only the always-visible prefix
+    lo[1], hi[1] = 2990, 5000      # 10 keys
+    for always, k in ((0, 128), (37, 128), (500, 7)):
+        idx, dist = oracle.knn_search_masked(codes, scales, queries, lo, hi, always, k)
+        # The brute force over the same allowed keys, written as one "cell" per query.
+        for qi in range(nq):
+            allowed = [g for g in range(n) if g < always or lo[qi] <= g < hi[qi]]
+            cs = np.array([0, len(allowed)], np.int64)
+            sel = np.array(allowed, np.int64)
+            widx, wdist = _brute_force(codes[sel], scales[sel], cs, queries[qi:qi + 1], np.zeros((1, 1), np.int32), k)
+            got = np.where(widx[0] >= 0, sel[np.maximum(widx[0], 0)], -1) if sel.size else widx[0]
+            np.testing.assert_array_equal(idx[qi], got)
+            np.testing.assert_array_equal(dist[qi], wdist[0])
+    idx, _ = oracle.knn_search_masked(codes, scales, queries, lo, hi, 0, 128)
+    assert np.all(idx[0] == -1)
+    assert sorted(idx[1][:10]) == list(range(2990, 3000)) and np.all(idx[1][10:] == -1)
+    # A range that is exactly one cell gives the IVF search's answer for that cell.
+    cs = np.array([0, 700, 1900, 3000], np.int64)
+    idx, dist = oracle.knn_search_masked(codes, scales, queries[:3], [700] * 3, [1900] * 3, 0, 128)
+    widx, wdist = oracle.knn_search(codes, scales, cs, queries[:3], np.ones((3, 1), np.int32), 128)
+    np.testing.assert_array_equal(idx, widx)
+    np.testing.assert_array_equal(dist, wdist)
+
+
+def test_query_quantisation_of_subnormal_queries():
+    rng = np.random.default_rng(42)
+    for scale in (2.0 ** -120, 2.0 ** -135, 2.0 ** -148):
+        q = (rng.standard_normal(256) * scale).astype(np.float32)
+        Q, prep = oracle.knn_prep_query(q)
+        mx = float(np.max(np.abs(q)))
+        e = math.frexp(mx)[1]
+        assert prep.qe == e - 14
+        err = np.abs(np.ldexp(Q.astype(np.float64), prep.qe) - q.astype(np.float64))
+        assert np.all(err <= np.ldexp(0.5, prep.qe))
+        assert np.max(np.abs(Q)) >= 8192
+
+
 def test_knn_integer_dot_is_exact_and_close_to_the_references_f16_scoring():
     d = 256
     rng = np.random.default_rng(11)
