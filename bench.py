@@ -686,6 +686,27 @@ def main():
             probe["cpu_baseline"] = pb.cpu_baseline()
         # search_ivf by nprobe: probe selection, then the scan of the selected cells (the store's cells are a
         # uniform assignment, unrelated to these centroids: the timing, not the recall, is the point).
+        # Masked exact search (search_tail's use): 256 queries, each over its own window of 81,920 keys
+        # (the IVF batch's mean keys per query) at a random place in the 125M-key store.
+        rng = np.random.default_rng(7)
+        lo = rng.integers(0, kb.N - 81920, (8, kb.NQ))
+        lohis = [torch.from_numpy(np.stack([l, l + 81920], 1).astype(np.int64)).to(dev) for l in lo]
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                kb.store.search_masked(kb.batches[i % 8]["q"], lohis[i % 8], 0, 128, out=kb.out)
+            torch.cuda.synchronize()
+            it = itertools.count()
+
+            def masked():
+                i = next(it)
+                kb.store.search_masked(kb.batches[i % 8]["q"], lohis[i % 8], 0, 128, out=kb.out)
+            mms = time_events(masked, args.steps, stream)
+        mbytes = kb.NQ * 81920 * (kb.D // 4 + 4)
+        extra["c5_knn_masked"] = dict(ms_per_batch=round(mms, 5), g_keys_per_s=round(kb.NQ * 81920 / mms / 1e6, 3),
+                                      roofline=dict(kernel="k_search<MASKED> (st_knn_search_masked_2bit)", bound="hbm",
+                                                    achieved=round(mbytes / mms / 1e6, 1), peak=PEAK["hbm_gbs"],
+                                                    unit="GB/s", frac=round(mbytes / mms / 1e6 / PEAK["hbm_gbs"], 4),
+                                                    traffic=None, algorithmic_bytes=int(mbytes)))
         kb.store.centroids = pb.c
         with torch.cuda.stream(stream):
             for i in range(args.warmup):

@@ -193,6 +193,12 @@ st_status st_attention_fused_bwd(const float *qkv, const float *ctx, const float
 st_status st_knn_quantize_2bit(const float *keys, int64_t n, int64_t d, uint8_t *codes,
                                float *scales, st_stream stream);
 
+/* gpu_step/knn.rs:216 (tile_of's norms): the per-key norm the reference
+ * stores with a quantised tile (and its cache file, knn/cache.rs:49), the sum
+ * over dims in order of f16((u - 1.5) * scale)^2 in f32; norms [n] device. */
+st_status st_knn_key_norms_2bit(const uint8_t *codes, const float *scales, int64_t n, int64_t d,
+                                float *norms, st_stream stream);
+
 /* gpu_step/knn/ivf.rs:466 `KnnStore::search_ivf`, the scored part
  * (scan_group ivf.rs:528-686: fused dequant-dot, top-k, merge, finalise),
  * given each query's probed cells.  The store holds keys cell-contiguous:

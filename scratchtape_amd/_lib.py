@@ -68,6 +68,7 @@ SIGNATURES = {
     "st_attention_fused_bwd": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "st_knn_quantize_2bit": [_vp, _i64, _i64, _vp, _vp, _vp],
     "st_knn_search_ivf_2bit": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
+    "st_knn_key_norms_2bit": [_vp, _vp, _i64, _i64, _vp, _vp],
     "st_knn_search_masked_2bit": [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_store_2bit": [_u64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_keys_f32": [_u64, _i64, _i64, _i64, _vp, _vp],

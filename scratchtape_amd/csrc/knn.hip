@@ -93,6 +93,28 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ keys
     quantize_row([&](int i) { return k[i]; }, d, codes + r * (d / 4), scales + r);
 }
 
+// The reference's stored per-key norm (knn.rs:216): sum over the dims, in
+// order, of f16((u - 1.5) scale)^2 in f32; one thread per key.
+__global__ __launch_bounds__(256) void k_key_norms(const uint8_t *__restrict__ codes, const float *__restrict__ scales,
+                                                   int64_t n, int32_t d, float *__restrict__ norms) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const uint8_t *row = codes + r * (d / 4);
+    const float s = scales[r];
+    float nrm = 0.f;
+    for (int i = 0; i < d; i++) {
+        const int u = (row[i >> 2] >> (2 * (i & 3))) & 3;
+        // The f32 product, then f16: the reference rounds twice.  The empty asm
+        // keeps the compiler from fusing the two into one mixed-precision FMA
+        // (a single rounding, which differs on f16 ties).
+        float p = ((float)u - 1.5f) * s;
+        asm volatile("" : "+v"(p));
+        const float v = (float)(_Float16)p;
+        nrm += v * v;
+    }
+    norms[r] = nrm;
+}
+
 // Counter-based N(0,1) generator for the synthetic store: a 64-bit mix of
 // (seed, row, pair index) gives two uniforms, Box-Muller gives two normals.
 __device__ __forceinline__ uint64_t mix64(uint64_t x) {
@@ -705,6 +727,21 @@ extern "C" st_status st_knn_quantize_2bit(const float *keys, int64_t n, int64_t 
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     hipLaunchKernelGGL(k_quantize, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st::stream_of(stream), keys, n,
                        (int32_t)d, codes, scales);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}
+
+extern "C" st_status st_knn_key_norms_2bit(const uint8_t *codes, const float *scales, int64_t n, int64_t d,
+                                           float *norms, st_stream stream) {
+    st::clear_error();
+    if (!codes || !scales || !norms) return st::fail(ST_ERR_INVALID, "key_norms: NULL buffer");
+    if (n < 0 || d <= 0 || d % 16 != 0)
+        return st::fail(ST_ERR_INVALID, "quantised keys need d %% 16 == 0 (got d = %lld)", (long long)d);
+    if (n == 0) return ST_OK;
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    if (cdiv(n, 256) > INT32_MAX) return st::fail(ST_ERR_INVALID, "key_norms: too many rows for one call");
+    hipLaunchKernelGGL(k_key_norms, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st::stream_of(stream), codes, scales,
+                       n, (int32_t)d, norms);
     ST_LAUNCH_CHECK();
     return ST_OK;
 }

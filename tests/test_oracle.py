@@ -670,3 +670,16 @@ def test_probe_is_covariant_under_centroid_permutation_and_full_sort_at_nprobe_n
     _, _, cnorm = oracle.knn_centroid_prep(cent)
     z = oracle.knn_probe(cent, np.zeros((1, 256), np.float32), nlist)
     np.testing.assert_array_equal(z[0], np.lexsort((np.arange(nlist), cnorm)))
+
+
+def test_quantizer_norm_is_the_f16_dequantised_norm_summed_in_order():
+    # knn.rs:216: sum over dims, in order, of f16((u - 1.5) * scale)^2 in f32.
+    rng = np.random.default_rng(43)
+    keys = rng.standard_normal((50, 256)).astype(np.float32)
+    keys[0] *= np.float32(1e-3)
+    keys[1] *= np.float32(300.0)
+    codes, scales, norms = oracle.quantize_2bit(keys, 256, with_norm=True)
+    u = _unpack(codes, 256)
+    deq = ((u.astype(np.float32) - np.float32(1.5)) * scales[:, None]).astype(np.float16).astype(np.float32)
+    want = np.cumsum(deq * deq, axis=1, dtype=np.float32)[:, -1]
+    np.testing.assert_array_equal(norms, want)
