@@ -72,6 +72,7 @@ __global__ __launch_bounds__(256) void k_softmax_bwd(const float *__restrict__ d
 }
 
 constexpr int LN_CHUNK = 128;  // rows per partial column sum
+constexpr int LN_REG = 16;     // row values held per lane (rows up to 1024 wide read once)
 
 // grid: ceil(rows / 4) workgroups of 4 row-waves.
 __global__ __launch_bounds__(256) void k_ln_fwd(const float *__restrict__ x, int64_t rows, int64_t d,
@@ -84,16 +85,39 @@ __global__ __launch_bounds__(256) void k_ln_fwd(const float *__restrict__ x, int
     const float *xr = x + r * d;
     const float *gm = params + off + (r / rows_pm) * stride, *bt = gm + d;
     const float inv_d = 1.0f / (float)d;
+    // Rows of up to 1024 columns are held in registers (16 per lane), so the
+    // row is read from memory once; wider rows re-read it.
+    float xv[LN_REG];
     float s = 0.f;
-    for (int64_t j = lane; j < d; j += 64) s += xr[j];
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        const int64_t j = lane + 64 * i;
+        xv[i] = j < d ? xr[j] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++)
+        if (lane + 64 * i < d) s += xv[i];
+    for (int64_t j = lane + 64 * LN_REG; j < d; j += 64) s += xr[j];
     const float mu = wave_sum(s) * inv_d;
     float sq = 0.f;
-    for (int64_t j = lane; j < d; j += 64) {
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        if (lane + 64 * i < d) {
+            const float c = xv[i] - mu;
+            sq += c * c;
+        }
+    }
+    for (int64_t j = lane + 64 * LN_REG; j < d; j += 64) {
         const float c = xr[j] - mu;
         sq += c * c;
     }
     const float sd = sqrtf(wave_sum(sq) * inv_d + eps);
-    for (int64_t j = lane; j < d; j += 64) y[r * d + j] = ((xr[j] - mu) / sd) * gm[j] + bt[j];
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        const int64_t j = lane + 64 * i;
+        if (j < d) y[r * d + j] = ((xv[i] - mu) / sd) * gm[j] + bt[j];
+    }
+    for (int64_t j = lane + 64 * LN_REG; j < d; j += 64) y[r * d + j] = ((xr[j] - mu) / sd) * gm[j] + bt[j];
     if (lane == 0) {
         mean[r] = mu;
         rstd[r] = 1.0f / sd;
@@ -111,8 +135,22 @@ __global__ __launch_bounds__(256) void k_ln_bwd_dx(const float *__restrict__ dy,
     const float *gm = params + off + (r / rows_pm) * stride;
     const float mu = mean[r], rs = rstd[r];
     const int64_t base = r * d;
+    float gv[LN_REG], hv[LN_REG];
     float s1 = 0.f, s2 = 0.f;
-    for (int64_t j = lane; j < d; j += 64) {
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        const int64_t j = lane + 64 * i;
+        gv[i] = j < d ? dy[base + j] * gm[j] : 0.f;
+        hv[i] = j < d ? (x[base + j] - mu) * rs : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        if (lane + 64 * i < d) {
+            s1 += gv[i];
+            s2 += gv[i] * hv[i];
+        }
+    }
+    for (int64_t j = lane + 64 * LN_REG; j < d; j += 64) {
         const float g = dy[base + j] * gm[j];
         s1 += g;
         s2 += g * ((x[base + j] - mu) * rs);
@@ -120,7 +158,15 @@ __global__ __launch_bounds__(256) void k_ln_bwd_dx(const float *__restrict__ dy,
     s1 = wave_sum(s1);
     s2 = wave_sum(s2);
     const float inv_d = 1.0f / (float)d;
-    for (int64_t j = lane; j < d; j += 64) {
+#pragma unroll
+    for (int i = 0; i < LN_REG; i++) {
+        const int64_t j = lane + 64 * i;
+        if (j < d) {
+            const float v = rs * (gv[i] - s1 * inv_d - hv[i] * (s2 * inv_d));
+            dx[base + j] = accumulate ? dx[base + j] + v : v;
+        }
+    }
+    for (int64_t j = lane + 64 * LN_REG; j < d; j += 64) {
         const float g = dy[base + j] * gm[j];
         const float xh = (x[base + j] - mu) * rs;
         const float v = rs * (g - s1 * inv_d - xh * (s2 * inv_d));
@@ -141,6 +187,7 @@ __global__ __launch_bounds__(256) void k_ln_bwd_part(const float *__restrict__ d
     const int64_t r1 = min(m * rows_pm + rows_pm, r0 + LN_CHUNK);
     float pg = 0.f, pb = 0.f;
     if (j < d) {
+#pragma unroll 4
         for (int64_t r = r0 + lane; r < r1; r += 4) {
             const float g = dy[r * d + j];
             pg += g * ((x[r * d + j] - mean[r]) * rstd[r]);
@@ -163,7 +210,15 @@ __global__ __launch_bounds__(256) void k_ln_bwd_sum(const float *__restrict__ pa
     const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
     if (j >= 2 * d) return;
     float s = 0.f;
-    for (int64_t c = 0; c < nch; c++) s += part[(m * nch + c) * 2 * d + j];
+    int64_t c = 0;
+    for (; c + 8 <= nch; c += 8) {  // eight loads in flight, added in chunk order
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = part[(m * nch + c + u) * 2 * d + j];
+#pragma unroll
+        for (int u = 0; u < 8; u++) s += v[u];
+    }
+    for (; c < nch; c++) s += part[(m * nch + c) * 2 * d + j];
     grads[off + m * stride + j] += s;
 }
 
