@@ -355,7 +355,8 @@ def bench_attention_fused(dev, stream, steps, warmup):
     nbytes = 4 * (2 * b * t * 3 * d + b * t * d + 2 * b * t * d + 2 * b * h * t + b * t * 3 * d)
     return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_ms=round(graph_ms, 5), fwd_ms=round(fwd_ms, 5),
                 bwd_ms=round(bwd_ms, 5), tflops=round(flops / graph_ms / 1e9, 3),
-                roofline=roofline("k_attn_fwd + k_attn_bwd (fused f16 attention step)", flops, nbytes, graph_ms))
+                roofline=roofline("k_attn_fwd + k_attn_bwd (fused f16 attention step)", flops, nbytes, graph_ms,
+                                  traffic_for("k_attn fused step", "scratchtape_amd/csrc/attn.hip")))
 
 
 def bench_layer_norm(dev, stream, steps, warmup):
@@ -388,7 +389,7 @@ def bench_layer_norm(dev, stream, steps, warmup):
     nbytes = 4 * (5 * n * d + 4 * n)
     return dict(rows=n, d=d, fwd_ms=round(fwd_ms, 5), graph_ms=round(graph_ms, 5),
                 roofline=roofline("k_ln_fwd + k_ln_bwd_dx + k_ln_bwd_part + k_ln_bwd_sum", 10 * n * d, nbytes,
-                                  graph_ms, route="f32"))
+                                  graph_ms, traffic_for("k_ln step", "scratchtape_amd/csrc/rows.hip"), route="f32"))
 
 
 def cpu_attention_baseline(reps=20):
@@ -706,7 +707,9 @@ def main():
                                       roofline=dict(kernel="k_search<MASKED> (st_knn_search_masked_2bit)", bound="hbm",
                                                     achieved=round(mbytes / mms / 1e6, 1), peak=PEAK["hbm_gbs"],
                                                     unit="GB/s", frac=round(mbytes / mms / 1e6 / PEAK["hbm_gbs"], 4),
-                                                    traffic=None, algorithmic_bytes=int(mbytes)))
+                                                    traffic=traffic_for("k_search masked",
+                                                                        "scratchtape_amd/csrc/knn.hip"),
+                                                    algorithmic_bytes=int(mbytes)))
         kb.store.centroids = pb.c
         with torch.cuda.stream(stream):
             for i in range(args.warmup):
