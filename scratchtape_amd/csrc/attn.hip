@@ -22,21 +22,23 @@
 // exp2; lse is stored in natural-log units).
 //
 // Design.  T <= 256 (T % 32 == 0) and hd = 64, so a problem's operands fit on
-// chip.  Work unit = one wave, which owns a pair of 16-row blocks {j, NB-1-j}
-// (causal work 1 + .. + NB balances to NB + 1 tiles per pair):
-//   forward   query-block pairs; S^T = K Q^T is computed so that each lane owns
+// chip.  Work unit = one wave, which owns one 16-row block j of its problem
+// (NB = T / 16 waves per workgroup, one workgroup per problem and role):
+//   forward   query block j; S^T = K Q^T is computed so that each lane owns
 //             one query column (row statistics need two shuffles), and its P^T
 //             tiles are directly the B operand of O^T = V^T P^T;
-//   backward  key-block pairs compute dK, dV (each lane owns one key column of
+//   backward  key block j computes dK, dV (each lane owns one key column of
 //             S = Q K^T and dP = dO V^T; P and dS are the B operands of
-//             dV^T = dO^T P and dK^T = Q^T dS); query-block pairs compute dQ
+//             dV^T = dO^T P and dK^T = Q^T dS); query block j computes dQ
 //             (lane owns a query column of S^T and dP^T; dS^T is the B operand
 //             of dQ^T = K^T dS^T).  No dS round trip through memory or LDS.
-// A workgroup (one to four waves, two workgroups per problem and role) first
-// loads its waves' own fragments, then stages the operands its waves share
-// into LDS as f16 (row-major and, where an operand is needed transposed, V^T,
-// Q^T, dO^T or K^T), with every load of a thread in flight at once; the MFMA
-// loops then read only LDS and registers.  Two 16-row tiles form the 32-deep k-chunk
+// A workgroup first loads its waves' own fragments, then stages the operands
+// its waves share into LDS as f16 (row-major and, where an operand is needed
+// transposed, V^T, Q^T, dO^T or K^T) once per problem, with every load of a
+// thread in flight at once; the MFMA loops then read only LDS and registers.
+// Causal work is uneven across the waves (block j has j + 1 tiles), so the
+// critical path is the last block's NB tiles; at T = 128 two waves share a
+// SIMD and the short blocks' waves fill the gaps of the long ones.  Two 16-row tiles form the 32-deep k-chunk
 // of an MFMA whose contraction runs over rows: element e of lane group g is
 // row 4g + e of the first tile (e < 4) or of the second (e >= 4), the order in
 // which the 16x16 accumulator layout hands them out; A and B agree on it.
@@ -69,18 +71,13 @@ __device__ __forceinline__ half8 ld_frag(const float *p) {
                  (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
 }
 
-// Work split of one problem: NB / 2 pairs of 16-row blocks {j, NB - 1 - j};
-// G workgroups per problem of W waves each, pair j on workgroup j % G, wave
-// j / G.
+// Shapes of a problem of T = 16 NB rows: NT threads (one wave per 16-row
+// block), LDS row pitch KP for row-major tiles and LDT for transposed ones
+// (8 halves of padding spread the rows over the LDS banks).
 template <int NB>
 struct Split {
-    static constexpr int P = NB / 2;
-    static constexpr int G = P < 2 ? P : 2;
-    static constexpr int W = (P + G - 1) / G;
-    static constexpr int NT = 64 * W;
-    static constexpr int T = NB * 16;
-    static constexpr int KP = HD + 8;   // row-major f16 tile row stride (halves)
-    static constexpr int LDT = T + 8;   // transposed f16 tile row stride (halves)
+    static constexpr int NT = 64 * NB;
+    static constexpr int T = NB * 16, KP = HD + 8, LDT = T + 8;
 };
 
 // Rows [0, n) (n % 32 == 0) of x (64 columns, row stride ld floats) into LDS
@@ -154,7 +151,7 @@ __device__ __forceinline__ half8 frag_t(const _Float16 *xt, int ldt, int row, in
 
 // Workgroup id -> (problem z, unit u in [0, U)), placing all U units of a
 // problem on one XCD (workgroups are dealt to the 8 XCDs round robin), so the
-// operand panels that several units stage are read from one L2:
+// operands that both backward roles stage are read from one L2:
 // id = (z / 8) 8U + 8u + z % 8.  False for the padding ids of a problem count
 // that is not a multiple of 8.
 __device__ __forceinline__ bool unit_of(int U, int64_t nz, int64_t &z, int &u) {
@@ -164,7 +161,7 @@ __device__ __forceinline__ bool unit_of(int U, int64_t nz, int64_t &z, int &u) {
     return z < nz;
 }
 
-// grid 8 G ceil(B*H / 8) (unit_of, G units per problem), W waves per workgroup.
+// grid 8 ceil(B*H / 8) (unit_of, one workgroup per problem), NB waves per workgroup.
 template <int NB>
 __global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restrict__ qkv, float *__restrict__ ctx,
                                                             float *__restrict__ lse, int32_t h, int64_t nz,
@@ -177,34 +174,23 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restr
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
     int64_t z;
     int x;
-    if (!unit_of(S::G, nz, z, x)) return;
-    const int j = __builtin_amdgcn_readfirstlane(x + S::G * (tid >> 6));  // this wave's pair
+    if (!unit_of(1, nz, z, x)) return;
+    const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's block
     const int64_t bb = z / h;
     const int hh = (int)(z % h);
     const int64_t D = (int64_t)h * HD, ld = 3 * D;
     const float *base = qkv + bb * T * ld + hh * HD;  // + 0: Q, + D: K, + 2D: V
 
     // This wave's query fragments (B operands) first, so their loads overlap the staging.
-    const int jj = j < S::P ? j : 0;
-    half8 qf[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const float *qrow = base + (int64_t)(16 * (u == 0 ? jj : NB - 1 - jj) + li) * ld;
-        qf[u][0] = ld_frag(qrow + 8 * g);
-        qf[u][1] = ld_frag(qrow + 32 + 8 * g);
-    }
-    // Keys of the workgroup's latest block's causal range, in whole 32-row chunks.
-    const int nk = (16 * (NB - x) + 31) & ~31;
-    stage<S::NT, T>(base + D, ld, nk, sK, KP, nullptr, 0, tid);
-    stage<S::NT, T>(base + 2 * D, ld, nk, nullptr, 0, sVt, LDT, tid);
+    const float *qrow = base + (int64_t)(16 * j + li) * ld;
+    const half8 q0 = ld_frag(qrow + 8 * g), q1 = ld_frag(qrow + 32 + 8 * g);
+    stage<S::NT, T>(base + D, ld, T, sK, KP, nullptr, 0, tid);
+    stage<S::NT, T>(base + 2 * D, ld, T, nullptr, 0, sVt, LDT, tid);
     __syncthreads();
-    if (j >= S::P) return;
 
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int qb = u == 0 ? j : NB - 1 - j;
+    {
+        const int qb = j;
         const int q = 16 * qb + li;  // this lane's query
-        const half8 q0 = qf[u][0], q1 = qf[u][1];
         // S^T over key-tile pairs (2 mm, 2 mm + 1), lane holding keys 16 kt + 4 g + r of query q,
         // kept as scale S log2(e) so that the softmax runs on 2^x.
         // The next pair's K fragments are read while this pair's products run; a pair's
@@ -292,9 +278,8 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restr
     }
 }
 
-// grid 16 G ceil(B*H / 8) (unit_of, 2 G units per problem: G computing dK, dV
-// over key-block pairs, then G computing dQ over query-block pairs), W waves
-// per workgroup.
+// grid 16 ceil(B*H / 8) (unit_of, two workgroups per problem: one computing
+// dK, dV by key block, one computing dQ by query block), NB waves per workgroup.
 template <int NB>
 __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restrict__ qkv,
                                                             const float *__restrict__ ctx,
@@ -311,10 +296,9 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
     int64_t z;
     int x;
-    if (!unit_of(2 * S::G, nz, z, x)) return;
-    const bool kv = x < S::G;
-    const int wg = kv ? x : x - S::G;
-    const int j = __builtin_amdgcn_readfirstlane(wg + S::G * (tid >> 6));  // this wave's pair
+    if (!unit_of(2, nz, z, x)) return;
+    const bool kv = x == 0;
+    const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's block
     const int64_t bb = z / h;
     const int hh = (int)(z % h);
     const int64_t D = (int64_t)h * HD, ld = 3 * D;
@@ -326,30 +310,17 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
 
     if (kv) {
         // This wave's key and value fragments (B operands) first.
-        const int jj = j < S::P ? j : 0;
-        half8 kf[2][2], vf[2][2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int64_t key = 16 * (u == 0 ? jj : NB - 1 - jj) + li;
-            kf[u][0] = ld_frag(base + D + key * ld + 8 * g);
-            kf[u][1] = ld_frag(base + D + key * ld + 32 + 8 * g);
-            vf[u][0] = ld_frag(base + 2 * D + key * ld + 8 * g);
-            vf[u][1] = ld_frag(base + 2 * D + key * ld + 32 + 8 * g);
-        }
-        // Queries from the workgroup's earliest key block on, in whole 32-row
-        // chunks; L and D = rowsum(dO o O) per query.
-        const int q0 = (16 * wg) & ~31;
-        stage<S::NT, T>(base + (int64_t)q0 * ld, ld, T - q0, sR0 + q0 * KP, KP, sT0 + q0, LDT, tid);
-        stage<S::NT, T>(dobase + (int64_t)q0 * D, D, T - q0, sR1 + q0 * KP, KP, sT1 + q0, LDT, tid,
-                        obase + (int64_t)q0 * D, D, sD + q0);
-        for (int r = q0 + tid; r < T; r += S::NT) sL[r] = lrow[r] * LOG2E;
+        const float *krow = base + D + (int64_t)(16 * j + li) * ld, *vrow = krow + D;
+        const half8 k0 = ld_frag(krow + 8 * g), k1 = ld_frag(krow + 32 + 8 * g);
+        const half8 v0 = ld_frag(vrow + 8 * g), v1 = ld_frag(vrow + 32 + 8 * g);
+        // Q, dO (row-major and transposed), L and D = rowsum(dO o O) of every query.
+        stage<S::NT, T>(base, ld, T, sR0, KP, sT0, LDT, tid);
+        stage<S::NT, T>(dobase, D, T, sR1, KP, sT1, LDT, tid, obase, D, sD);
+        for (int r = tid; r < T; r += S::NT) sL[r] = lrow[r] * LOG2E;
         __syncthreads();
-        if (j >= S::P) return;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int kb = u == 0 ? j : NB - 1 - j;
+        {
+            const int kb = j;
             const int key = 16 * kb + li;  // this lane's key
-            const half8 k0 = kf[u][0], k1 = kf[u][1], v0 = vf[u][0], v1 = vf[u][1];
             f32x4 dv[4], dk[4];
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) dv[ht] = dk[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -394,12 +365,10 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
     } else {
         // This wave's query and upstream-gradient fragments (B operands), D and
         // L of its queries first, so their loads overlap the staging.
-        const int jj = j < S::P ? j : 0;
-        half8 qf[2][2], df[2][2];
-        float dq_d[2], dq_l[2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int64_t q = 16 * (u == 0 ? jj : NB - 1 - jj) + li;
+        half8 q0, q1, d0, d1;
+        float dsum = 0.f, L;
+        {
+            const int64_t q = 16 * j + li;
             const float *qr = base + q * ld, *dr = dobase + q * D, *orr = obase + q * D;
             float4 dv[4], ov[4];
 #pragma unroll
@@ -408,31 +377,26 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
                 dv[2 * c + 1] = *reinterpret_cast<const float4 *>(dr + 32 * c + 8 * g + 4);
                 ov[2 * c] = *reinterpret_cast<const float4 *>(orr + 32 * c + 8 * g);
                 ov[2 * c + 1] = *reinterpret_cast<const float4 *>(orr + 32 * c + 8 * g + 4);
-                qf[u][c] = ld_frag(qr + 32 * c + 8 * g);
-                df[u][c] = half8{(_Float16)dv[2 * c].x, (_Float16)dv[2 * c].y, (_Float16)dv[2 * c].z,
-                                 (_Float16)dv[2 * c].w, (_Float16)dv[2 * c + 1].x, (_Float16)dv[2 * c + 1].y,
-                                 (_Float16)dv[2 * c + 1].z, (_Float16)dv[2 * c + 1].w};
             }
-            float dsum = 0.f;
+            q0 = ld_frag(qr + 8 * g);
+            q1 = ld_frag(qr + 32 + 8 * g);
+            d0 = half8{(_Float16)dv[0].x, (_Float16)dv[0].y, (_Float16)dv[0].z, (_Float16)dv[0].w,
+                       (_Float16)dv[1].x, (_Float16)dv[1].y, (_Float16)dv[1].z, (_Float16)dv[1].w};
+            d1 = half8{(_Float16)dv[2].x, (_Float16)dv[2].y, (_Float16)dv[2].z, (_Float16)dv[2].w,
+                       (_Float16)dv[3].x, (_Float16)dv[3].y, (_Float16)dv[3].z, (_Float16)dv[3].w};
 #pragma unroll
             for (int k = 0; k < 4; k++) dsum += dv[k].x * ov[k].x + dv[k].y * ov[k].y + dv[k].z * ov[k].z + dv[k].w * ov[k].w;
             dsum += __shfl_xor(dsum, 16, 64);
             dsum += __shfl_xor(dsum, 32, 64);
-            dq_d[u] = dsum;
-            dq_l[u] = lrow[q] * LOG2E;
+            L = lrow[q] * LOG2E;
         }
-        // Keys of the workgroup's latest query block's causal range.
-        const int nk = (16 * (NB - wg) + 31) & ~31;
-        stage<S::NT, T>(base + D, ld, nk, sR0, KP, sT0, LDT, tid);
-        stage<S::NT, T>(base + 2 * D, ld, nk, sR1, KP, nullptr, 0, tid);
+        // K (row-major and transposed) and V of every key.
+        stage<S::NT, T>(base + D, ld, T, sR0, KP, sT0, LDT, tid);
+        stage<S::NT, T>(base + 2 * D, ld, T, sR1, KP, nullptr, 0, tid);
         __syncthreads();
-        if (j >= S::P) return;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int qb = u == 0 ? j : NB - 1 - j;
+        {
+            const int qb = j;
             const int q = 16 * qb + li;  // this lane's query
-            const half8 q0 = qf[u][0], q1 = qf[u][1], d0 = df[u][0], d1 = df[u][1];
-            const float dsum = dq_d[u], L = dq_l[u];
             f32x4 dq[4];
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) dq[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -474,7 +438,7 @@ template <int NB>
 void launch_fwd(const float *qkv, float *ctx, float *lse, int64_t b, int64_t h, float scale, int32_t one,
                 hipStream_t s) {
     const int64_t nz = b * h;
-    hipLaunchKernelGGL(k_attn_fwd<NB>, dim3((unsigned)(8 * Split<NB>::G * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0, s,
+    hipLaunchKernelGGL(k_attn_fwd<NB>, dim3((unsigned)(8 * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0, s,
                        qkv, ctx, lse, (int32_t)h, nz, scale, one);
 }
 
@@ -482,7 +446,7 @@ template <int NB>
 void launch_bwd(const float *qkv, const float *ctx, const float *dctx, const float *lse, float *dqkv, int64_t b,
                 int64_t h, float scale, hipStream_t s) {
     const int64_t nz = b * h;
-    hipLaunchKernelGGL(k_attn_bwd<NB>, dim3((unsigned)(16 * Split<NB>::G * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0,
+    hipLaunchKernelGGL(k_attn_bwd<NB>, dim3((unsigned)(16 * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0,
                        s, qkv, ctx, dctx, lse, dqkv, (int32_t)h, nz, scale);
 }
 
