@@ -25,6 +25,8 @@
 #include <algorithm>
 #include <cstring>
 #include <numeric>
+#include <queue>
+#include <utility>
 #include <vector>
 
 #include "dma_tile.h"
@@ -72,9 +74,16 @@ struct GProb {
     int32_t pad;
 };
 
+// Units per XCD list that the host-computed schedule covers.
+constexpr int SCHED_MAX = 128;
+
 struct GroupArgs {
     GProb p[st::GROUP_MAX];
     int32_t count;
+    // 1: owner[x][i] is the workgroup (0 .. L-1 of XCD x's L) that runs unit i
+    // of x's list; 0: round robin (workgroup w runs units w, w + L, ..).
+    int32_t sched;
+    uint8_t owner[XCDS][SCHED_MAX];
 };
 static_assert(sizeof(GroupArgs) <= 4000, "kernel arguments");
 
@@ -95,51 +104,87 @@ __device__ __forceinline__ int64_t slot_src_rt(bool kc, int p, int64_t ld, int r
     return kc ? slot_src<ROWS, true>(p, ld, row0) : slot_src<ROWS, false>(p, ld, row0);
 }
 
-// Unit j of XCD x's list (every GEMM's block of tiles for XCD x, in order).
-template <class C>
-__device__ void locate(const GroupArgs &ga, int x, int j, int wave, int lane, Unit<C> &u) {
-    u.p = -1;
-    int t = 0;
-    for (int p = 0; p < ga.count; p++) {
-        const int U = ga.p[p].units;
-        const int s0 = (int)((int64_t)x * U / XCDS), s1 = (int)((int64_t)(x + 1) * U / XCDS);
-        if (j < s1 - s0) {
-            u.p = p;
-            t = s0 + j;
-            break;
+// A wave-uniform value read from LDS, moved to scalar registers.
+__device__ __forceinline__ int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+template <class T>
+__device__ __forceinline__ T *uni(T *v) {
+    return reinterpret_cast<T *>(uni(reinterpret_cast<int64_t>(v)));
+}
+
+// First unit of XCD x's block of GEMM p's units: x U / 8 of U.
+__device__ __forceinline__ int block_start(int x, int units) { return (int)((int64_t)x * units / XCDS); }
+
+// The group's arguments in LDS (copied from the kernel-argument segment once
+// per workgroup: a read of it whose index is only known at run time goes to
+// memory, one dependent round trip per read) and cum[p] = the position in XCD
+// x's list of GEMM p's block (cum[count] = the list's length).
+__device__ __forceinline__ void load_args(const GroupArgs &ga, GroupArgs &sga, int32_t *cum, int x, int tid,
+                                          int nthreads) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(&ga);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(&sga);
+    for (int i = tid; i < (int)(sizeof(GroupArgs) / 4); i += nthreads) dst[i] = src[i];
+    __syncthreads();
+    if (tid < 64) {
+        const int p = tid, count = sga.count;
+        const int U = p < count ? sga.p[p].units : 0;
+        int v = block_start(x + 1, U) - block_start(x, U);  // inclusive prefix sum over p
+#pragma unroll
+        for (int d = 1; d < st::GROUP_MAX; d *= 2) {
+            const int w = __shfl_up(v, d, 64);
+            if (p >= d) v += w;
         }
-        j -= s1 - s0;
+        if (p < count) cum[p + 1] = v;
+        if (p == 0) cum[0] = 0;
     }
+    __syncthreads();
+}
+
+// Unit j of XCD x's list (every GEMM's block of tiles for XCD x, in order):
+// the GEMM is the number of blocks that end at or before j (one ballot).
+template <class C>
+__device__ void locate(const GroupArgs &ga, const int32_t *cum, int x, int j, int wave, int lane, Unit<C> &u) {
+    const int count = ga.count;
+    const bool before = lane < count && cum[lane + 1] <= j;
+    const int p = __popcll(__ballot(before));
+    u.p = p < count ? p : -1;
     if (u.p < 0) return;
-    const GProb &g = ga.p[u.p];
-    const int bx = t % g.tiles_n;
-    const int r = t / g.tiles_n;
-    const int by = r % g.tiles_m;
-    const int zs = r / g.tiles_m;
-    u.zb = zs / g.splits;
-    u.slice = zs % g.splits;
+    const GProb &g = ga.p[p];
+    const int tiles_n = uni(g.tiles_n), tiles_m = uni(g.tiles_m), splits = uni(g.splits), slice_k = uni(g.slice_k);
+    const int flags = uni(g.flags), lda = uni(g.lda), ldb = uni(g.ldb);
+    const int t = block_start(x, uni(g.units)) + j - uni(cum[p]);
+    const int bx = t % tiles_n;
+    const int r = t / tiles_n;
+    const int by = r % tiles_m;
+    const int zs = r / tiles_m;
+    u.zb = zs / splits;
+    u.slice = zs % splits;
     u.row0 = by * C::TM;
     u.col0 = bx * TN;
-    const int kbeg = u.slice * g.slice_k;
-    u.nst = (min(g.k, kbeg + g.slice_k) - kbeg) / BK;
-    u.akc = !(g.flags & F_TA);
-    u.bkc = (g.flags & F_TB) != 0;
-    u.anext = reinterpret_cast<const char *>(g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner) +
-                                             (u.akc ? kbeg : (int64_t)kbeg * g.lda));
-    u.bnext = reinterpret_cast<const char *>(g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner) +
-                                             (u.bkc ? kbeg : (int64_t)kbeg * g.ldb));
+    const int kbeg = u.slice * slice_k;
+    u.nst = (min(uni(g.k), kbeg + slice_k) - kbeg) / BK;
+    u.akc = !(flags & F_TA);
+    u.bkc = (flags & F_TB) != 0;
+    u.anext = uni(reinterpret_cast<const char *>(g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner) +
+                                                 (u.akc ? kbeg : (int64_t)kbeg * lda)));
+    u.bnext = uni(reinterpret_cast<const char *>(g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner) +
+                                                 (u.bkc ? kbeg : (int64_t)kbeg * ldb)));
     // Wave-load i of this wave fills LDS 1024 i bytes after the wave's first;
     // its sources lie at least 1024 i bytes past the base (rows >= 8 i apart
     // at ld >= 32, or k-lines >= i apart at ld >= 256; the leading dimensions
     // are checked on the host), so the offsets stay non-negative.
 #pragma unroll
     for (int i = 0; i < C::LA; i++)
-        u.aoff[i] = (uint32_t)(4 * slot_src_rt<C::TM>(u.akc, (wave * C::LA + i) * 64 + lane, g.lda, u.row0) - 1024 * i);
+        u.aoff[i] = (uint32_t)(4 * slot_src_rt<C::TM>(u.akc, (wave * C::LA + i) * 64 + lane, lda, u.row0) - 1024 * i);
 #pragma unroll
     for (int i = 0; i < C::LB; i++)
-        u.boff[i] = (uint32_t)(4 * slot_src_rt<TN>(u.bkc, (wave * C::LB + i) * 64 + lane, g.ldb, u.col0) - 1024 * i);
-    u.astep = 4 * (u.akc ? BK : (int64_t)BK * g.lda);
-    u.bstep = 4 * (u.bkc ? BK : (int64_t)BK * g.ldb);
+        u.boff[i] = (uint32_t)(4 * slot_src_rt<TN>(u.bkc, (wave * C::LB + i) * 64 + lane, ldb, u.col0) - 1024 * i);
+    u.astep = 4 * (u.akc ? BK : (int64_t)BK * lda);
+    u.bstep = 4 * (u.bkc ? BK : (int64_t)BK * ldb);
 }
 
 // grid: a multiple of 8 workgroups, at most one per CU (the ring takes most
@@ -149,17 +194,35 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
     constexpr int TM = C::TM, NS = C::NS, SA = C::SA, SB = C::SB, LA = C::LA, LB = C::LB;
     constexpr int WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
     __shared__ __attribute__((aligned(16))) float lds[NS * (SA + SB)];
+    __shared__ GroupArgs sga;
+    __shared__ int32_t cum[st::GROUP_MAX + 1];
+    static_assert(NS * (SA + SB) * 4 + sizeof(GroupArgs) + 4 * (st::GROUP_MAX + 1) <= 160 * 1024, "LDS");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / C::WGN, wn = wave % C::WGN;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int x = blockIdx.x % XCDS, L = gridDim.x / XCDS;
-    int j = blockIdx.x / XCDS;
+    const int w = blockIdx.x / XCDS;
+    load_args(ga, sga, cum, x, tid, C::THREADS);
+
+    // Position in x's list of this workgroup's first unit after position
+    // `prev` (prev = -1: its first), or the list's length if none is left.
+    const int nlist = uni(cum[sga.count]), sched = uni(sga.sched);
+    auto next_pos = [&](int prev) -> int {
+        if (!sched) return min(prev < 0 ? w : prev + L, nlist);
+        for (int base = prev + 1; base < nlist; base += 64) {
+            const int i = base + lane;
+            const uint64_t mine = __ballot(i < nlist && sga.owner[x][i] == w);
+            if (mine) return base + __builtin_ctzll(mine);
+        }
+        return nlist;
+    };
+    int j = next_pos(-1), jn = next_pos(j);
 
     Unit<C> cur, nxt;
-    locate(ga, x, j, wave, lane, cur);
+    locate(sga, cum, x, j, wave, lane, cur);
     if (cur.p < 0) return;
-    locate(ga, x, j + L, wave, lane, nxt);
+    locate(sga, cum, x, jn, wave, lane, nxt);
 
     // The ring advances one slot per stage: islot is the byte offset of the
     // slot the next issued stage fills, rslot of the next stage to land.
@@ -178,8 +241,9 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 
     f32x4 acc[FM][FN];
     while (true) {
-        const GProb &g = ga.p[cur.p];
-        const bool do_cs = (g.flags & F_CS) && cur.row0 == 0;
+        const GProb &g = sga.p[cur.p];
+        const int gflags = uni(g.flags), gsplits = uni(g.splits);
+        const bool do_cs = (gflags & F_CS) && cur.row0 == 0;
         float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < TN), this slice
 #pragma unroll
         for (int i = 0; i < FM; i++)
@@ -267,8 +331,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
         }
 
         if (do_cs && tid < TN) {
-            if (g.splits > 1)
-                g.cs[(cur.zb * g.splits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
+            if (gsplits > 1)
+                g.cs[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
             else
                 g.cs[cur.zb * g.cs_stride + cur.col0 + tid] += cs_acc;
         }
@@ -284,11 +348,12 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
         {
             constexpr int EP = WN + 4;
             float *ep = lds + (rslot == 0 ? NS * SLOT : rslot) / 4 - (SA + SB) + wave * 16 * EP;
-            const bool split = g.splits > 1;
-            float *const P = split ? g.out + (cur.zb * g.splits + cur.slice) * (int64_t)g.m * g.n : nullptr;
-            const int64_t o0 = split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner);
-            const int64_t ld = split ? g.n : g.ldo;
-            float *const obase = split ? P : g.out + o0;
+            const bool split = gsplits > 1;
+            float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
+            const int64_t o0 = uni(split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner));
+            const int64_t ld = uni((int64_t)(split ? g.n : g.ldo));
+            float *const obase = uni(split ? P : g.out + o0);
+            const float *const bias = uni(g.bias), *const mask = uni(g.mask), *const res = uni(g.res);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
 #pragma unroll
@@ -302,23 +367,23 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                     const int grow = cur.row0 + wm * WM + i * 16 + row, gcol = cur.col0 + wn * WN + c4;
                     const int64_t idx = (int64_t)grow * ld + gcol;
                     if (!split) {
-                        if (g.bias) {
-                            const float *bp = g.bias + cur.zb * g.bias_stride + gcol;
+                        if (bias) {
+                            const float *bp = bias + cur.zb * g.bias_stride + gcol;
 #pragma unroll
                             for (int x = 0; x < 4; x++) v[x] += bp[x];
                         }
-                        if (g.flags & F_RELU) {
+                        if (gflags & F_RELU) {
 #pragma unroll
                             for (int x = 0; x < 4; x++) v[x] = v[x] < 0.f ? 0.f : v[x];
                         }
-                        if (g.mask) {
-                            const f32x4 mk = *reinterpret_cast<const f32x4 *>(g.mask + o0 + idx);
+                        if (mask) {
+                            const f32x4 mk = *reinterpret_cast<const f32x4 *>(mask + o0 + idx);
 #pragma unroll
                             for (int x = 0; x < 4; x++)
                                 if (mk[x] <= 0.f) v[x] = 0.f;
                         }
-                        if (g.res) v += *reinterpret_cast<const f32x4 *>(g.res + o0 + idx);
-                        if (g.flags & F_ACC) v += *reinterpret_cast<const f32x4 *>(obase + idx);
+                        if (res) v += *reinterpret_cast<const f32x4 *>(res + o0 + idx);
+                        if (gflags & F_ACC) v += *reinterpret_cast<const f32x4 *>(obase + idx);
                     }
                     *reinterpret_cast<f32x4 *>(obase + idx) = v;
                 }
@@ -327,8 +392,9 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 
         if (nxt.p < 0) break;
         cur = nxt;
-        j += L;
-        locate(ga, x, j + L, wave, lane, nxt);
+        j = jn;
+        jn = next_pos(j);
+        locate(sga, cum, x, jn, wave, lane, nxt);
     }
 }
 
@@ -347,12 +413,20 @@ struct SumArgs {
 };
 
 // The split GEMMs' partial sums, one thread per 4 outputs (then one per
-// column sum), as k_sum_slices; thread ranges per GEMM start at t0.
+// column sum), as k_sum_slices; thread ranges per GEMM start at t0.  The
+// arguments are copied to LDS first (as in k_gemm_group).
 __global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
+    __shared__ SumArgs ssa;
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(&sa);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(&ssa);
+        for (int i = threadIdx.x; i < (int)(sizeof(SumArgs) / 4); i += 256) dst[i] = src[i];
+        __syncthreads();
+    }
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int p = 0;
-    while (p + 1 < sa.count && e >= sa.p[p + 1].t0) p++;
-    const SProb &s = sa.p[p];
+    while (p + 1 < ssa.count && e >= ssa.p[p + 1].t0) p++;
+    const SProb &s = ssa.p[p];
     const int64_t local = e - s.t0;
     if (local < 0) return;
     if (local < s.batch * s.mn4) {
@@ -415,6 +489,47 @@ bool group_tall(const DmaGemm &d) { return d.m % Tall::TM == 0; }
 }  // namespace st
 
 namespace {
+
+// Each XCD's list of units (every GEMM's block, in kernel order) assigned to
+// its L workgroups longest-processing-time first: unit by unit, in list order
+// (GEMMs sorted by k-stages per unit, longest first), to the workgroup with
+// the least work so far (the lowest index on ties), a unit costing its
+// k-stages plus EPI_STAGES for its epilogue.  Round robin when a list is
+// longer than SCHED_MAX.  Which workgroup runs a unit never changes its
+// arithmetic.
+constexpr int EPI_STAGES = 2;
+
+void schedule(GroupArgs &ga, int L) {
+    ga.sched = 0;
+    if (L > 255) return;
+    for (int x = 0; x < XCDS; x++) {
+        int64_t n = 0;
+        for (int o = 0; o < ga.count; o++)
+            n += (int64_t)(x + 1) * ga.p[o].units / XCDS - (int64_t)x * ga.p[o].units / XCDS;
+        if (n > SCHED_MAX) return;
+    }
+    typedef std::pair<int64_t, int> Load;  // (k-stages so far, workgroup): the smallest pops first
+    for (int x = 0; x < XCDS; x++) {
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> q;
+        for (int w = 0; w < L; w++) q.push(Load(0, w));
+        int i = 0;
+        for (int o = 0; o < ga.count; o++) {
+            const GProb &g = ga.p[o];
+            const int s0 = (int)((int64_t)x * g.units / XCDS), s1 = (int)((int64_t)(x + 1) * g.units / XCDS);
+            for (int t = s0; t < s1; t++) {
+                const int slice = (t / g.tiles_n / g.tiles_m) % g.splits;
+                const int kbeg = slice * g.slice_k;
+                const int nst = (std::min(g.k, kbeg + g.slice_k) - kbeg) / BK;
+                Load l = q.top();
+                q.pop();
+                ga.owner[x][i++] = (uint8_t)l.second;
+                l.first += nst + EPI_STAGES;
+                q.push(l);
+            }
+        }
+    }
+    ga.sched = 1;
+}
 
 template <class C>
 st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_t stream) {
@@ -542,6 +657,7 @@ st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_
         }
     }
     const int64_t wgs = std::min<int64_t>(cus / XCDS * XCDS, cdiv(units, XCDS) * XCDS);
+    schedule(ga, (int)std::max<int64_t>(1, wgs / XCDS));
     void (*kern)(GroupArgs) = f16 ? &k_gemm_group<C, true> : &k_gemm_group<C, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)std::max<int64_t>(XCDS, wgs)), dim3(C::THREADS), 0, stream, ga);
     hipError_t e = hipGetLastError();
