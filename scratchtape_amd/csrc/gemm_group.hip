@@ -496,10 +496,25 @@ namespace {
 // the least work so far (the lowest index on ties), a unit costing its
 // k-stages plus EPI_STAGES for its epilogue.  Round robin when a list is
 // longer than SCHED_MAX.  Which workgroup runs a unit never changes its
-// arithmetic.
+// arithmetic.  The last schedule is kept per host thread with the shapes it
+// was made for, so a group issued again with the same shapes reuses it.
 constexpr int EPI_STAGES = 2;
 
 void schedule(GroupArgs &ga, int L) {
+    thread_local std::vector<int32_t> last_key;
+    thread_local uint8_t last_owner[XCDS][SCHED_MAX];
+    thread_local int32_t last_sched = 0;
+    std::vector<int32_t> key = {L, ga.count};
+    for (int o = 0; o < ga.count; o++) {
+        const GProb &g = ga.p[o];
+        key.insert(key.end(), {g.units, g.tiles_n, g.tiles_m, g.splits, g.slice_k, g.k});
+    }
+    if (key == last_key) {
+        ga.sched = last_sched;
+        std::memcpy(ga.owner, last_owner, sizeof last_owner);
+        return;
+    }
+    last_key.clear();  // invalid until this schedule is complete
     ga.sched = 0;
     if (L > 255) return;
     for (int x = 0; x < XCDS; x++) {
@@ -529,6 +544,9 @@ void schedule(GroupArgs &ga, int L) {
         }
     }
     ga.sched = 1;
+    last_sched = 1;
+    std::memcpy(last_owner, ga.owner, sizeof last_owner);
+    last_key = std::move(key);
 }
 
 template <class C>
