@@ -120,6 +120,23 @@ def time_events(fn, reps, stream):
     return s.elapsed_time(e) / reps
 
 
+def time_graph_steps(fn, steps, stream):
+    """The K timed steps captured as ONE HIP graph (each step's calls in full, in order), replayed once between
+    HIP events: ms per step, without the launch overhead a separate graph per step pays (several us each)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(steps):
+            fn()
+    g.replay()  # untimed: the graph's first replay
+    torch.cuda.synchronize()
+    ms = time_events(g.replay, 1, stream) / steps
+    del g
+    return ms
+
+
 def time_graph(fn, steps, warmup, stream):
     """Captures fn() into a HIP graph; returns (ms per replay, graph)."""
     import torch
@@ -203,7 +220,8 @@ class StepSet:
 
 def bench_gemm_set(dev, stream, steps, warmup, use_f16):
     """Times the set three ways: one grouped call (the headline), step order (forward one by one, backward
-    pairs grouped) and one call per GEMM; each eager (HIP events around the calls) and as a HIP graph."""
+    pairs grouped) and one call per GEMM; each eager (HIP events around the calls), as one HIP graph per step
+    replayed `steps` times, and as one HIP graph of all `steps` steps (the headline timing)."""
     import torch
     ss = StepSet(dev)
     modes = {"grouped": ss.grouped_fn(use_f16), "step_order": ss.step_order_fn(use_f16),
@@ -216,8 +234,9 @@ def bench_gemm_set(dev, stream, steps, warmup, use_f16):
             torch.cuda.synchronize()
             eager = time_events(fn, steps, stream)
             graph, _ = time_graph(fn, steps, warmup, stream)
-            times[name] = dict(eager_ms=round(eager, 5), graph_ms=round(graph, 5),
-                               tflops=round(ss.flops / graph / 1e9, 2))
+            steps_ms = time_graph_steps(fn, steps, stream)
+            times[name] = dict(eager_ms=round(eager, 5), graph_per_step_ms=round(graph, 5),
+                               graph_ms=round(steps_ms, 5), tflops=round(ss.flops / steps_ms / 1e9, 2))
         modes["grouped"]()  # the outputs the parity check reads come from the grouped launch
         torch.cuda.synchronize()
         per_call = []
@@ -323,10 +342,11 @@ def bench_attention(dev, stream, steps, warmup, use_f16):
         for _ in range(warmup):
             step()
         eager_ms = time_events(step, steps, stream)
-        graph_ms, _ = time_graph(step, steps, warmup, stream)
+        per_step_ms, _ = time_graph(step, steps, warmup, stream)
+        graph_ms = time_graph_steps(step, steps, stream)
     flops = 6 * b * h * 2 * t * t * hd
-    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_ms=round(graph_ms, 5),
-                tflops=round(flops / graph_ms / 1e9, 3))
+    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_per_step_ms=round(per_step_ms, 5),
+                graph_ms=round(graph_ms, 5), tflops=round(flops / graph_ms / 1e9, 3))
 
 
 def bench_attention_fused(dev, stream, steps, warmup):
@@ -349,11 +369,13 @@ def bench_attention_fused(dev, stream, steps, warmup):
         eager_ms = time_events(step, steps, stream)
         fwd_ms = time_events(fwd, steps, stream)
         bwd_ms = time_events(bwd, steps, stream)
-        graph_ms, _ = time_graph(step, steps, warmup, stream)
+        per_step_ms, _ = time_graph(step, steps, warmup, stream)
+        graph_ms = time_graph_steps(step, steps, stream)
     flops = 6 * b * h * 2 * t * t * hd  # the six products of the unfused step, for comparison
     # Algorithmic bytes: qkv read by both passes, dctx, ctx written then read, lse, dqkv written.
     nbytes = 4 * (2 * b * t * 3 * d + b * t * d + 2 * b * t * d + 2 * b * h * t + b * t * 3 * d)
-    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_ms=round(graph_ms, 5), fwd_ms=round(fwd_ms, 5),
+    return dict(flops=flops, eager_ms=round(eager_ms, 5), graph_per_step_ms=round(per_step_ms, 5),
+                graph_ms=round(graph_ms, 5), fwd_ms=round(fwd_ms, 5),
                 bwd_ms=round(bwd_ms, 5), tflops=round(flops / graph_ms / 1e9, 3),
                 roofline=roofline("k_attn_fwd + k_attn_bwd (fused f16 attention step)", flops, nbytes, graph_ms,
                                   traffic_for("k_attn fused step", "scratchtape_amd/csrc/attn.hip")))
@@ -384,10 +406,12 @@ def bench_layer_norm(dev, stream, steps, warmup):
         for _ in range(warmup):
             step()
         fwd_ms = time_events(fwd, steps, stream)
-        graph_ms, _ = time_graph(step, steps, warmup, stream)
+        per_step_ms, _ = time_graph(step, steps, warmup, stream)
+        graph_ms = time_graph_steps(step, steps, stream)
     # Algorithmic bytes: x read and y written (forward); dy and x read, dx written (backward); mean, rstd.
     nbytes = 4 * (5 * n * d + 4 * n)
-    return dict(rows=n, d=d, fwd_ms=round(fwd_ms, 5), graph_ms=round(graph_ms, 5),
+    return dict(rows=n, d=d, fwd_ms=round(fwd_ms, 5), graph_per_step_ms=round(per_step_ms, 5),
+                graph_ms=round(graph_ms, 5),
                 roofline=roofline("k_ln_fwd + k_ln_bwd_dx + k_ln_bwd_part + k_ln_bwd_sum", 10 * n * d, nbytes,
                                   graph_ms, traffic_for("k_ln step", "scratchtape_amd/csrc/rows.hip"), route="f32"))
 
@@ -610,7 +634,8 @@ def main():
         graph16 = t16["grouped"]["graph_ms"]
         value = ss16.flops / graph16 / 1e9
         # The dominant kernel is the grouped launch itself (k_gemm_group, plus the split-k sum k_sum_group):
-        # the set's flops and algorithmic bytes over its time per graph replay, from HIP events on its stream.
+        # the set's flops and algorithmic bytes over its time per step with the K timed steps replayed as one
+        # HIP graph, from HIP events on its stream.
         roof = roofline("k_gemm_group f16 (+ k_sum_group): the 15-GEMM set in one grouped call", ss16.flops,
                         ss16.bytes, graph16,
                         traffic_for("k_gemm_group f16 step set", "scratchtape_amd/csrc/gemm_group.hip"))
