@@ -38,6 +38,7 @@ constexpr int D = 256;              // vector width (the scan's key width)
 constexpr int BLK = 8;              // vectors per digit block
 constexpr int BLK_BYTES = BLK * 2 * D;  // 4096
 constexpr int PROBE_MAX = 16;       // ivf.rs:126
+constexpr int PER_MAX = 8;          // centroid blocks per dots workgroup (staged in LDS)
 constexpr int64_t DD_BUDGET = 256ll << 20;  // bytes of dd per query chunk
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
@@ -100,16 +101,19 @@ __global__ __launch_bounds__(256) void k_probe_prep(const float *__restrict__ x,
 // dd[q][c] for queries [q0, q0 + nqc) of the chunk (digit blocks qdig, exponents
 // qex, chunk-relative) against centroids [0, nlist).  grid.y: groups of 8 query
 // blocks (wave w takes blocks 8 y + 2 w and + 1); grid.x: slices of `per`
-// centroid blocks.
+// (<= PER_MAX) centroid blocks, which the workgroup stages in LDS (digits,
+// norms, exponents: every load in flight at once) before its waves walk them.
 __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ qdig, const int32_t *__restrict__ qex,
                                                     int32_t nqc, const int8_t *__restrict__ cdig,
                                                     const int32_t *__restrict__ cexp, const double *__restrict__ cnorm,
                                                     int32_t nlist, int32_t per, double *__restrict__ dd) {
+    __shared__ v4i s_dig[PER_MAX * BLK_BYTES / 16];
+    __shared__ double s_cn[PER_MAX * BLK];
+    __shared__ int32_t s_ce[PER_MAX * BLK];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int nqb = (nqc + BLK - 1) / BLK;
     const int qb0 = blockIdx.y * 8 + 2 * w;
-    if (qb0 >= nqb) return;
-    const bool two = qb0 + 1 < nqb;
+    const bool active = qb0 < nqb, two = qb0 + 1 < nqb;
     const int ncb = (nlist + BLK - 1) / BLK;
     const int cb0 = blockIdx.x * per;
     const int cb1 = min(cb0 + per, ncb);
@@ -117,10 +121,25 @@ __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ q
     v4i a[2][4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        a[0][s] = *reinterpret_cast<const v4i *>(qdig + (int64_t)qb0 * BLK_BYTES + s * 1024 + lane * 16);
+        a[0][s] = active ? *reinterpret_cast<const v4i *>(qdig + (int64_t)qb0 * BLK_BYTES + s * 1024 + lane * 16)
+                         : v4i{0, 0, 0, 0};
         a[1][s] = two ? *reinterpret_cast<const v4i *>(qdig + (int64_t)(qb0 + 1) * BLK_BYTES + s * 1024 + lane * 16)
                       : v4i{0, 0, 0, 0};
     }
+    {
+        const int nb = cb1 - cb0;
+        const v4i *src = reinterpret_cast<const v4i *>(cdig + (int64_t)cb0 * BLK_BYTES);
+#pragma unroll
+        for (int i = 0; i < PER_MAX; i++)
+            if (i < nb) s_dig[i * 256 + threadIdx.x] = src[i * 256 + threadIdx.x];
+        if (threadIdx.x < nb * BLK) {
+            const int c = cb0 * BLK + threadIdx.x;
+            s_cn[threadIdx.x] = c < nlist ? cnorm[c] : 0.0;
+            s_ce[threadIdx.x] = c < nlist ? cexp[c] : 0;
+        }
+    }
+    __syncthreads();
+    if (!active) return;
     const bool odd = lane & 1;
     const int qv = 2 * (lane >> 4) + (lane & 1);  // query within a block
     const int cv = (lane & 15) >> 1;              // centroid within a block
@@ -133,18 +152,14 @@ __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ q
         qe[u] = qok[u] ? qex[qi] : 0;
     }
 
-    v4i b[4], bn[4];
-    if (cb0 < cb1) {
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-            b[s] = *reinterpret_cast<const v4i *>(cdig + (int64_t)cb0 * BLK_BYTES + s * 1024 + lane * 16);
-    }
+#pragma unroll 1
     for (int cb = cb0; cb < cb1; cb++) {
-        if (cb + 1 < cb1) {
+        const int k = cb - cb0;
+        v4i b[4];
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-                bn[s] = *reinterpret_cast<const v4i *>(cdig + (int64_t)(cb + 1) * BLK_BYTES + s * 1024 + lane * 16);
-        }
+        for (int s = 0; s < 4; s++) b[s] = s_dig[k * 256 + s * 64 + lane];
+        const double cn = s_cn[k * BLK + cv];
+        const int ce = s_ce[k * BLK + cv];
         v4i acc[2];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
@@ -154,8 +169,6 @@ __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ q
         }
         const int c = cb * BLK + cv;
         const bool cok = c < nlist;
-        const double cn = cok ? cnorm[c] : 0.0;
-        const int ce = cok ? cexp[c] : 0;
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             // Lane l holds rows 4 (l/16) .. + 3 (queries 2 (l/16) and + 1, digits
@@ -173,10 +186,6 @@ __global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ q
                 const int64_t qi = (int64_t)(qb0 + u) * BLK + qv;
                 dd[qi * nlist + c] = cn - ldexp((double)dot, qe[u] + ce + 1);
             }
-        }
-        if (cb + 1 < cb1) {
-#pragma unroll
-            for (int s = 0; s < 4; s++) b[s] = bn[s];
         }
     }
 }
@@ -477,6 +486,7 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
         const int64_t gy = cdiv(cdiv(nqc, BLK), 8);
         int64_t per = cdiv(ncb * gy, 1024);
         if (per < 2) per = 2;
+        if (per > PER_MAX) per = PER_MAX;
         const int64_t gx = cdiv(ncb, per);
         hipLaunchKernelGGL(k_probe_dots, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, qdig, qex, (int32_t)nqc,
                            digits, cexp, cnorm, (int32_t)nlist, (int32_t)per, dd);
