@@ -121,8 +121,27 @@ def lib():
         L.orc_knn_centroid_prep.argtypes = [_f32p, _i64, _i64, _i16p, _i32p, _f64p]
         L.orc_knn_probe.argtypes = [_i16p, _i32p, _f64p, _i64, _f32p, _i64, _i64, _i64, _i32p]
         L.orc_knn_ref_f16_dist.restype = ctypes.c_float
+        L.orc_set_threads.argtypes = [_i32]
+        L.orc_get_threads.restype = _i32
         _lib = L
     return _lib
+
+
+class threads:
+    """Context manager: matmul, transpose and knn_search split their rows (queries) over n OpenMP threads inside
+    the block (1 outside, the reference's single-threaded path).  Results are the same for every n; only the
+    all-cores CPU baseline uses more than one."""
+
+    def __init__(self, n: int):
+        self.n = max(1, int(n))
+
+    def __enter__(self):
+        self.old = lib().orc_get_threads()
+        lib().orc_set_threads(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_threads(self.old)
 
 
 # --------------------------------------------------------------------------- Rng (nn.rs:8-35)

@@ -7,9 +7,16 @@
  * CPU baseline timed by the benchmark.  Nothing in the product library links,
  * loads or calls it.
  *
- * Build: gcc -O3 -mavx2 -mfma -ffp-contract=off -fPIC -shared (see Makefile).
- * -ffp-contract=off matters: Rust never contracts a*b+c into an FMA, so the
- * restated loops must keep every multiply and add separately rounded.
+ * Build: gcc -O3 -mavx2 -mfma -ffp-contract=off -fopenmp -fPIC -shared (see
+ * Makefile).  -ffp-contract=off matters: Rust never contracts a*b+c into an
+ * FMA, so the restated loops must keep every multiply and add separately
+ * rounded.
+ *
+ * Threads: orc_matmul, orc_transpose and orc_knn_search split their rows (or
+ * queries) over orc_set_threads(n) OpenMP threads (1 by default, the
+ * reference's single-threaded CPU path).  Each output element is computed by
+ * one thread in the same order as with one, so the results do not depend on
+ * the thread count; more threads only serve the all-cores CPU baseline.
  *
  * Pinning of every function (which test pins it and how) is listed in the
  * header comment of oracle/__init__.py.
@@ -18,6 +25,12 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+static int g_threads = 1;
+
+void orc_set_threads(int32_t n) { g_threads = n < 1 ? 1 : n; }
+
+int32_t orc_get_threads(void) { return g_threads; }
 
 /* ------------------------------------------------------------------------ */
 /* Rng: xorshift64 (13, 7, 17), src/nn.rs:8-35.                              */
@@ -68,6 +81,7 @@ void orc_rng_fill_gaussian(uint64_t *s, int64_t n, float scale, float *out) {
 void orc_matmul(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n) {
     const int64_t BLOCK = 64;
     memset(out, 0, sizeof(float) * (size_t)(m * n));
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
     for (int64_t i0 = 0; i0 < m; i0 += BLOCK) {
         int64_t i_max = i0 + BLOCK < m ? i0 + BLOCK : m;
         for (int64_t p0 = 0; p0 < k; p0 += BLOCK) {
@@ -86,6 +100,7 @@ void orc_matmul(const float *a, const float *b, float *out, int64_t m, int64_t k
 
 /* tensor.rs:278-287: [m, n] -> [n, m]. */
 void orc_transpose(const float *a, float *out, int64_t m, int64_t n) {
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1)
     for (int64_t i = 0; i < m; i++)
         for (int64_t j = 0; j < n; j++) out[j * m + i] = a[i * n + j];
 }
@@ -522,9 +537,10 @@ void orc_knn_search(const uint8_t *codes, const float *scales, const int64_t *ce
                     const float *queries, const int32_t *probes, int64_t nq, int64_t nprobe,
                     int64_t d, int64_t k, int64_t *out_idx, float *out_dist) {
     int64_t kb = d / 4;
-    int16_t *Q = (int16_t *)malloc(sizeof(int16_t) * (size_t)d);
-    uint64_t *heap = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)k);
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
     for (int64_t qi = 0; qi < nq; qi++) {
+        int16_t *Q = (int16_t *)malloc(sizeof(int16_t) * (size_t)d);
+        uint64_t *heap = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)(k > 0 ? k : 1));
         orc_qprep prep;
         orc_knn_prep_query(queries + qi * d, d, Q, &prep);
         int64_t size = 0;
@@ -567,9 +583,9 @@ void orc_knn_search(const uint8_t *codes, const float *scales, const int64_t *ce
                 out_idx[qi * k + j] = -1;
             }
         }
+        free(heap);
+        free(Q);
     }
-    free(heap);
-    free(Q);
 }
 
 /* The masked exact search (knn.rs:295-331 search_tagged / search_tail, the

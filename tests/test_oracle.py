@@ -505,6 +505,28 @@ def test_knn_search_equals_brute_force_and_handles_edges():
     assert np.all(idx[0][5:] == -1) and np.all(np.isinf(dist[0][5:]))
 
 
+def test_thread_count_does_not_change_results():
+    """The all-cores CPU baseline runs the same oracle over several threads: matmul, transpose and knn_search
+    split rows (queries) only, so their outputs are bit-identical to the single-threaded ones."""
+    rng = np.random.default_rng(77)
+    a = rng.standard_normal((300, 130)).astype(np.float32)
+    b = rng.standard_normal((130, 70)).astype(np.float32)
+    one = oracle.matmul(a, b), oracle.transpose(a)
+    d, ncells, nq = 256, 10, 13
+    sizes = rng.integers(50, 300, ncells)
+    cell_start = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    codes, scales = oracle.quantize_2bit(rng.standard_normal((cell_start[-1], d)).astype(np.float32), d)
+    queries = rng.standard_normal((nq, d)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, 3, replace=False) for _ in range(nq)]).astype(np.int32)
+    one_knn = oracle.knn_search(codes, scales, cell_start, queries, probes, 128)
+    with oracle.threads(4):
+        many = oracle.matmul(a, b), oracle.transpose(a)
+        many_knn = oracle.knn_search(codes, scales, cell_start, queries, probes, 128)
+    assert oracle.lib().orc_get_threads() == 1
+    for x, y in zip(one + one_knn, many + many_knn):
+        np.testing.assert_array_equal(x, y)
+
+
 def test_knn_masked_search_equals_brute_force_over_the_allowed_keys():
     d, n, nq = 256, 3000, 12
     rng = np.random.default_rng(41)
