@@ -628,6 +628,38 @@ class ProbeBench:
                            "integer distances + top-8 in the oracle (C, 1 pinned thread)")
 
 
+# --------------------------------------------------------------------------- device ceilings
+
+def device_ceilings(dev, stream):
+    """Measured ceilings beside the published peaks every roofline is priced against: the matrix cores with only
+    independent MFMA chains in flight (two waves per SIMD, 8 chains each), a plain streaming read of 1 GiB, and the
+    device's CU count and clocks (HIP device attributes)."""
+    import ctypes
+    import torch
+    from scratchtape_amd import _lib
+    vals = [ctypes.c_int32() for _ in range(4)]
+    _lib.call("st_device_info", *[ctypes.byref(v) for v in vals])
+    cus, clk, mclk, bus = (v.value for v in vals)
+    out = dict(cus=cus, clock_mhz=clk / 1e3, mem_clock_mhz=mclk / 1e3, mem_bus_bits=bus)
+    blocks, iters, chains, waves = 2 * cus, 20000, 8, 4
+    sink = torch.zeros(8 * cus, device=dev)
+    with torch.cuda.stream(stream):
+        for kind, name, per in ((0, "f16", 16384), (1, "f32", 2048), (2, "i8", 32768)):
+            f = lambda: _lib.call("st_peak_mfma", kind, iters, blocks, sink.data_ptr(), stream.cuda_stream)
+            f()
+            ms = time_events(f, 5, stream)
+            out[f"mfma_{name}_tflops_measured"] = round(blocks * waves * chains * iters * per / ms / 1e9, 1)
+        buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        g = lambda: _lib.call("st_peak_read", buf.data_ptr(), buf.numel() * 4, 8 * cus, sink.data_ptr(),
+                              stream.cuda_stream)
+        g()
+        ms = time_events(g, 10, stream)
+        out["hbm_read_gbs_measured"] = round(buf.numel() * 4 / ms / 1e6, 1)
+        del buf
+    out["published_peaks"] = dict(PEAK)
+    return out
+
+
 # --------------------------------------------------------------------------- main
 
 def main():
@@ -661,7 +693,7 @@ def main():
     torch.cuda.init()
     stream = torch.cuda.Stream(device=dev)
     prop = torch.cuda.get_device_properties(dev)
-    extra = {"device": prop.name, "cus": prop.multi_processor_count, "host_cpu": cpu_model(), "nproc": os.cpu_count()}
+    extra = {"device": {"name": prop.name}, "host_cpu": cpu_model(), "nproc": os.cpu_count()}
     result = None
 
     if args.only in ("all", "gemm"):
@@ -801,6 +833,8 @@ def main():
         del kb
         torch.cuda.empty_cache()
 
+    log("[bench] device ceilings")
+    extra["device"].update(device_ceilings(dev, stream))
     result["extra"] = extra
     print(json.dumps(result), flush=True)
 

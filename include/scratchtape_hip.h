@@ -272,6 +272,23 @@ st_status st_knn_synth_store_2bit(uint64_t seed, int64_t row0, int64_t n, int64_
 st_status st_knn_synth_keys_f32(uint64_t seed, int64_t row0, int64_t n, int64_t d, float *keys,
                                 st_stream stream);
 
+/* ---- Device ceilings (benchmark support, no reference counterpart) ------- */
+
+/* The current device's CU count, shader clock and memory clock (kHz) and
+ * memory bus width (bits), from the HIP device attributes. */
+st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *mem_clock_khz, int32_t *mem_bus_bits);
+
+/* `blocks` workgroups of 4 waves, each wave running 8 independent MFMA chains
+ * of `iters` steps: kind 0 v_mfma_f32_16x16x32_f16 (16384 FLOP per step),
+ * 1 v_mfma_f32_16x16x4_f32 (2048), 2 v_mfma_i32_16x16x64_i8 (32768 OP).
+ * The caller times it; `sink` ([blocks] floats) is never written in practice
+ * (a guarded store keeps the chains live). */
+st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink, st_stream stream);
+
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) of src once with `blocks`
+ * grid-stride workgroups; `sink` as for st_peak_mfma. */
+st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks, float *sink, st_stream stream);
+
 /* ---- Misc ---------------------------------------------------------------- */
 
 /* Message of the last failed call on this thread ("" if none). */

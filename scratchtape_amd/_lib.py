@@ -75,6 +75,9 @@ SIGNATURES = {
     "st_knn_centroid_digit_bytes": [_i64, _i64],
     "st_knn_centroids_prep": [_vp, _i64, _i64, _vp, _vp, _vp, _vp],
     "st_knn_probe": [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp],
+    "st_device_info": [_vp, _vp, _vp, _vp],
+    "st_peak_mfma": [_i32, _i64, _i32, _vp, _vp],
+    "st_peak_read": [_vp, _i64, _i32, _vp, _vp],
     "st_last_error": [],
     "st_sync": [_vp],
     "st_version": [],

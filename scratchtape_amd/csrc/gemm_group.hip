@@ -36,6 +36,8 @@ namespace {
 
 using namespace dma;
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
 constexpr int XCDS = 8;
 constexpr int TN = 128;  // output tile columns (both shapes)
 
@@ -239,16 +241,30 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 #pragma unroll
     for (int st = 0; st < NS - 1; st++) issue(cur);
 
+    // Accumulators: the f32 route's 16 x 16 blocks (v_mfma_f32_16x16x4_f32), or
+    // the f16 route's 32 x 32 blocks (v_mfma_f32_32x32x16_f16, which on gfx950
+    // does twice the work of v_mfma_f32_16x16x32_f16 in the same issue time).
+    constexpr int M32 = WM / 32, N32 = WN / 32;
     f32x4 acc[FM][FN];
+    f32x16 acc2[M32][N32];
     while (true) {
         const GProb &g = sga.p[cur.p];
         const int gflags = uni(g.flags), gsplits = uni(g.splits);
         const bool do_cs = (gflags & F_CS) && cur.row0 == 0;
         float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < TN), this slice
+        if constexpr (F16) {
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+            for (int i = 0; i < M32; i++)
 #pragma unroll
-            for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int jn = 0; jn < N32; jn++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc2[i][jn][e] = 0.f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 
         // Stage st of cur: wait for this wave's DMA of it (younger stages,
         // possibly the next unit's, stay in flight), barrier (every wave's
@@ -272,26 +288,36 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                 const float *lb = la + SA;
                 const int gq = lane >> 4;
                 if constexpr (F16) {
-                    half8 af[FM], bf[FN];
+                    // 32 x 32 x 16 operands: lane l holds row (or column) l % 32
+                    // and the 8 k of group 2 ks + l / 32 of the stage.
+                    half8 af[M32][2], bf[N32][2];
+                    const int r32 = lane & 31, h = lane >> 5;
 #pragma unroll
-                    for (int i = 0; i < FM; i++) {
-                        float v[8];
-                        frag<TM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, v);
+                    for (int i = 0; i < M32; i++)
 #pragma unroll
-                        for (int e = 0; e < 8; e++) af[i][e] = (_Float16)v[e];
-                    }
+                        for (int ks = 0; ks < 2; ks++) {
+                            float v[8];
+                            frag<TM, AKC>(la, wm * WM + i * 32 + r32, 2 * ks + h, v);
 #pragma unroll
-                    for (int jn = 0; jn < FN; jn++) {
-                        float v[8];
-                        frag<TN, BKC>(lb, wn * WN + jn * 16 + (lane & 15), gq, v);
+                            for (int e = 0; e < 8; e++) af[i][ks][e] = (_Float16)v[e];
+                        }
 #pragma unroll
-                        for (int e = 0; e < 8; e++) bf[jn][e] = (_Float16)v[e];
-                    }
+                    for (int jn = 0; jn < N32; jn++)
 #pragma unroll
-                    for (int i = 0; i < FM; i++)
+                        for (int ks = 0; ks < 2; ks++) {
+                            float v[8];
+                            frag<TN, BKC>(lb, wn * WN + jn * 32 + r32, 2 * ks + h, v);
 #pragma unroll
-                        for (int jn = 0; jn < FN; jn++)
-                            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+                            for (int e = 0; e < 8; e++) bf[jn][ks][e] = (_Float16)v[e];
+                        }
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                        for (int i = 0; i < M32; i++)
+#pragma unroll
+                            for (int jn = 0; jn < N32; jn++)
+                                acc2[i][jn] =
+                                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][ks], bf[jn][ks], acc2[i][jn], 0, 0, 0);
                 } else {
                     float ax[FM][8], bx8[FN][8];
 #pragma unroll
@@ -346,7 +372,9 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
         // mask <= 0, + residual, + out.
         bar();
         {
-            constexpr int EP = WN + 4;
+            // Pitch: 16 banks between the 4-row groups of a 16 x 16 block, 32
+            // between the two lane halves of a 32 x 32 block.
+            constexpr int EP = F16 ? WN + 8 : WN + 4;
             float *ep = lds + (rslot == 0 ? NS * SLOT : rslot) / 4 - (SA + SB) + wave * 16 * EP;
             const bool split = gsplits > 1;
             float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
@@ -356,10 +384,22 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
             const float *const bias = uni(g.bias), *const mask = uni(g.mask), *const res = uni(g.res);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
+                if constexpr (F16) {
+                    // Rows 16 (i % 2) .. + 15 of 32 x 32 block i / 2: element e
+                    // of a lane is row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
 #pragma unroll
-                for (int jn = 0; jn < FN; jn++)
+                    for (int jn = 0; jn < N32; jn++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) ep[(4 * (lane >> 4) + r) * EP + jn * 16 + (lane & 15)] = acc[i][jn][r];
+                        for (int e = 0; e < 8; e++)
+                            ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * EP + jn * 32 + (lane & 31)] =
+                                acc2[i >> 1][jn][8 * (i & 1) + e];
+                } else {
+#pragma unroll
+                    for (int jn = 0; jn < FN; jn++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            ep[(4 * (lane >> 4) + r) * EP + jn * 16 + (lane & 15)] = acc[i][jn][r];
+                }
 #pragma unroll
                 for (int q = 0; q < 16 * WN / 4 / 64; q++) {
                     const int e = q * 64 + lane, row = e / (WN / 4), c4 = (e % (WN / 4)) * 4;

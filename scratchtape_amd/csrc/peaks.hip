@@ -1,0 +1,112 @@
+// Device ceilings for the benchmark's roofline context (no reference
+// counterpart, on no data path): the matrix cores' throughput with nothing but
+// independent MFMA chains in flight, the HBM read rate of a plain streaming
+// kernel, and the device's CU count and clocks.  The benchmark reports these
+// beside the published peaks it prices every kernel against.
+#include "common.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+
+constexpr int CHAINS = 8;  // independent accumulators per wave (covers the MFMA latency)
+
+// Never true for the values these kernels accumulate; the guarded store keeps
+// every chain's result live without writing memory.
+constexpr float NEVER = -1.2345e30f;
+
+// kind 0: v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x4_f32,
+// 2: v_mfma_i32_16x16x64_i8.  Operands come from the lane id so that nothing
+// folds; magnitudes stay small, so no accumulator overflows or turns inf.
+template <int KIND>
+__global__ __launch_bounds__(256) void k_peak_mfma(int64_t iters, float *__restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.f;
+    if constexpr (KIND == 0) {
+        half8 a, b;
+        for (int e = 0; e < 8; e++) {
+            a[e] = (_Float16)(1e-3f * (float)((lane + e) & 7));
+            b[e] = (_Float16)(1e-3f * (float)((lane * 3 + e) & 7));
+        }
+        f32x4 acc[CHAINS];
+        for (int c = 0; c < CHAINS; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int64_t i = 0; i < iters; i++) {
+#pragma unroll
+            for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[c], 0, 0, 0);
+        }
+        for (int c = 0; c < CHAINS; c++) s += acc[c][0] + acc[c][3];
+    } else if constexpr (KIND == 1) {
+        const float a = 1e-3f * (float)(lane & 7), b = 1e-3f * (float)((lane * 3) & 7);
+        f32x4 acc[CHAINS];
+        for (int c = 0; c < CHAINS; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int64_t i = 0; i < iters; i++) {
+#pragma unroll
+            for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[c], 0, 0, 0);
+        }
+        for (int c = 0; c < CHAINS; c++) s += acc[c][0] + acc[c][3];
+    } else {
+        const v4i a = {lane & 1, (lane >> 1) & 1, 0, 1}, b = {1, 0, lane & 1, 0};
+        v4i acc[CHAINS];
+        for (int c = 0; c < CHAINS; c++) acc[c] = v4i{0, 0, 0, 0};
+        for (int64_t i = 0; i < iters; i++) {
+#pragma unroll
+            for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
+        }
+        for (int c = 0; c < CHAINS; c++) s += (float)(acc[c][0] + acc[c][3]);
+    }
+    if (s == NEVER) sink[blockIdx.x] = s;
+}
+
+// Reads src [n4] float4 once (grid-stride, four loads in flight per thread).
+__global__ __launch_bounds__(256) void k_peak_read(const float4 *__restrict__ src, int64_t n4,
+                                                   float *__restrict__ sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    float acc = 0.f;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+        const float4 v0 = src[i], v1 = src[i + stride], v2 = src[i + 2 * stride], v3 = src[i + 3 * stride];
+        acc += (v0.x + v1.y) + (v2.z + v3.w);
+    }
+    for (; i < n4; i += stride) acc += src[i].x;
+    if (acc == NEVER) sink[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *mem_clock_khz,
+                                    int32_t *mem_bus_bits) {
+    st::clear_error();
+    if (!cus || !clock_khz || !mem_clock_khz || !mem_bus_bits) return st::fail(ST_ERR_INVALID, "device_info: NULL");
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    int dev = 0;
+    ST_HIP_CHECK(hipGetDevice(&dev));
+    ST_HIP_CHECK(hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev));
+    ST_HIP_CHECK(hipDeviceGetAttribute(clock_khz, hipDeviceAttributeClockRate, dev));
+    ST_HIP_CHECK(hipDeviceGetAttribute(mem_clock_khz, hipDeviceAttributeMemoryClockRate, dev));
+    ST_HIP_CHECK(hipDeviceGetAttribute(mem_bus_bits, hipDeviceAttributeMemoryBusWidth, dev));
+    return ST_OK;
+}
+
+extern "C" st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink, st_stream stream) {
+    st::clear_error();
+    if (kind < 0 || kind > 2) return st::fail(ST_ERR_INVALID, "peak_mfma: kind is 0 (f16), 1 (f32) or 2 (i8)");
+    if (iters < 1 || blocks < 1 || !sink) return st::fail(ST_ERR_INVALID, "peak_mfma: bad iters, blocks or sink");
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    void (*k)(int64_t, float *) = kind == 0 ? k_peak_mfma<0> : kind == 1 ? k_peak_mfma<1> : k_peak_mfma<2>;
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st::stream_of(stream), iters, sink);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}
+
+extern "C" st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks, float *sink, st_stream stream) {
+    st::clear_error();
+    if (!src || !sink || bytes < 16 || bytes % 16 || blocks < 1 || (reinterpret_cast<uintptr_t>(src) & 15))
+        return st::fail(ST_ERR_INVALID, "peak_read: need a 16-byte aligned buffer of a multiple of 16 bytes");
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    hipLaunchKernelGGL(k_peak_read, dim3((unsigned)blocks), dim3(256), 0, st::stream_of(stream),
+                       reinterpret_cast<const float4 *>(src), bytes / 16, sink);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}

@@ -135,3 +135,14 @@ def test_masked_search_arguments_are_validated():
         _lib.ST_ERR_INVALID
     assert L.st_knn_search_masked_2bit(fake, fake, 1000, fake, fake, 0, 4, 256, 129, fake, fake, None) == \
         _lib.ST_ERR_INVALID
+
+
+def test_ceiling_probe_arguments_are_validated():
+    L = scratchtape_amd.lib()
+    fake = 1 << 20
+    assert L.st_peak_mfma(3, 10, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert b"kind" in L.st_last_error()
+    assert L.st_peak_mfma(0, 0, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_peak_read(fake, 24, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_peak_read(fake + 4, 32, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_device_info(None, None, None, None) == _lib.ST_ERR_INVALID
