@@ -132,9 +132,11 @@ def time_events(fn, reps, stream):
     return s.elapsed_time(e) / reps
 
 
-def time_graph_steps(fn, steps, stream):
-    """The K timed steps captured as ONE HIP graph (each step's calls in full, in order), replayed once between
-    HIP events: ms per step, without the launch overhead a separate graph per step pays (several us each)."""
+def time_graph_steps(fn, steps, stream, reps=5, spread=None):
+    """The K timed steps captured as ONE HIP graph (each step's calls in full, in order): ms per step, without the
+    launch overhead a separate graph per step pays (several us each).  The graph is replayed `reps` times, each
+    replay (exactly K steps) timed on its own between HIP events; the median replay is reported (min and max go
+    into `spread` when given)."""
     import torch
     fn()
     torch.cuda.synchronize()
@@ -144,9 +146,11 @@ def time_graph_steps(fn, steps, stream):
             fn()
     g.replay()  # untimed: the graph's first replay
     torch.cuda.synchronize()
-    ms = time_events(g.replay, 1, stream) / steps
+    per = sorted(time_events(g.replay, 1, stream) / steps for _ in range(reps))
     del g
-    return ms
+    if spread is not None:
+        spread.update(min_ms=round(per[0], 5), max_ms=round(per[-1], 5), replays=reps)
+    return per[len(per) // 2]
 
 
 def time_graph(fn, steps, warmup, stream):
@@ -246,9 +250,11 @@ def bench_gemm_set(dev, stream, steps, warmup, use_f16):
             torch.cuda.synchronize()
             eager = time_events(fn, steps, stream)
             graph, _ = time_graph(fn, steps, warmup, stream)
-            steps_ms = time_graph_steps(fn, steps, stream)
+            spread = {}
+            steps_ms = time_graph_steps(fn, steps, stream, spread=spread)
             times[name] = dict(eager_ms=round(eager, 5), graph_per_step_ms=round(graph, 5),
-                               graph_ms=round(steps_ms, 5), tflops=round(ss.flops / steps_ms / 1e9, 2))
+                               graph_ms=round(steps_ms, 5), graph_spread=spread,
+                               tflops=round(ss.flops / steps_ms / 1e9, 2))
         modes["grouped"]()  # the outputs the parity check reads come from the grouped launch
         torch.cuda.synchronize()
         per_call = []

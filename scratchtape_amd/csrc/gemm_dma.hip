@@ -1,7 +1,8 @@
 // GEMM on gfx950 with operand tiles moved global -> LDS by the DMA path of
 // global_load_lds_dwordx4: no register staging, NS - 1 k-stages in flight, one
-// barrier per stage.  f16-in/f32-accumulate (v_mfma_f32_16x16x32_f16, f32
-// rounded to f16 to nearest even when a fragment is read from LDS) and f32
+// barrier per stage.  f16-in/f32-accumulate (v_mfma_f32_32x32x16_f16, f32
+// rounded to f16 to nearest even when a fragment is read from LDS; on gfx950
+// it does twice the work of v_mfma_f32_16x16x32_f16 per issue) and f32
 // (v_mfma_f32_16x16x4_f32).  Semantics: gpu_step/matmul.rs:26-299 (MatRef
 // addressing, the epilogue in the reference's order, deterministic split-k).
 //
@@ -48,7 +49,11 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
     constexpr int LA = BM / 32, LB = BN / 32;  // DMA wave-loads per wave per stage
     constexpr int SA = BM * BK, SB = BN * BK;  // floats per stage
-    constexpr int TP = BN + 4;                 // row pitch of the staged output tile
+    // Row pitch of the staged output tile: 16 banks between the 4-row groups of
+    // a 16 x 16 block, 32 between the two lane halves of a 32 x 32 block.
+    constexpr int TP = F16 ? BN + 8 : BN + 4;
+    constexpr int M32 = WM / 32, N32 = WN / 32;
+    static_assert(!F16 || (M32 >= 1 && N32 >= 1), "32 x 32 blocks per wave");
     static_assert(BM * TP <= NS * (SA + SB), "output tile fits the stage ring");
     __shared__ __attribute__((aligned(16))) float lds[NS * (SA + SB)];
 
@@ -90,11 +95,21 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
         for (int j = 0; j < LB; j++) dma16(bbase + boff[j] + st * bstep, base + SA * 4 + (wave_u * LB + j) * 1024);
     };
 
-    f32x4 acc[FM][FN];
+    f32x4 acc[FM][FN];      // f32 route: 16 x 16 blocks
+    f32x16 acc2[M32][N32];  // f16 route: 32 x 32 blocks
+    if constexpr (F16) {
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+        for (int i = 0; i < M32; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < N32; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc2[i][j][e] = 0.f;
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < BN), this slice
 
     // Stage st lives in ring slot st % NS.  Per stage: wait for this wave's DMA
@@ -109,26 +124,35 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
         const float *lb = la + SA;
         const int gq = lane >> 4;
         if constexpr (F16) {
-            half8 af[FM], bf[FN];
+            // 32 x 32 x 16 operands: lane l holds row (or column) l % 32 and
+            // the 8 k of group 2 ks + l / 32 of the stage.
+            half8 af[M32][2], bf[N32][2];
+            const int r32 = lane & 31, h = lane >> 5;
 #pragma unroll
-            for (int i = 0; i < FM; i++) {
-                float x[8];
-                frag<BM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, x);
+            for (int i = 0; i < M32; i++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) af[i][e] = (_Float16)x[e];
-            }
+                for (int ks = 0; ks < 2; ks++) {
+                    float x[8];
+                    frag<BM, AKC>(la, wm * WM + i * 32 + r32, 2 * ks + h, x);
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
-                float x[8];
-                frag<BN, BKC>(lb, wn * WN + j * 16 + (lane & 15), gq, x);
+                    for (int e = 0; e < 8; e++) af[i][ks][e] = (_Float16)x[e];
+                }
 #pragma unroll
-                for (int e = 0; e < 8; e++) bf[j][e] = (_Float16)x[e];
-            }
+            for (int j = 0; j < N32; j++)
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int ks = 0; ks < 2; ks++) {
+                    float x[8];
+                    frag<BN, BKC>(lb, wn * WN + j * 32 + r32, 2 * ks + h, x);
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    for (int e = 0; e < 8; e++) bf[j][ks][e] = (_Float16)x[e];
+                }
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int i = 0; i < M32; i++)
+#pragma unroll
+                    for (int j = 0; j < N32; j++)
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][ks], bf[j][ks], acc2[i][j], 0, 0, 0);
         } else {
             // Lane group gq supplies k = 8 gq + u at MFMA step u, for A and B alike.
             float ax[FM][8], bx8[FN][8];
@@ -173,13 +197,25 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
     // 16-byte runs of rows to memory, with the epilogue in the reference's
     // order: + bias, ReLU, zero where mask <= 0, + residual, + out.
     bar();  // every wave is done with the stage ring
+    if constexpr (F16) {
+        // Element e of a lane of a 32 x 32 block: row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+        for (int i = 0; i < M32; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++)
+            for (int j = 0; j < N32; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                lds[(wm * WM + i * 16 + 4 * (lane >> 4) + r) * TP + wn * WN + j * 16 + (lane & 15)] = acc[i][j][r];
+                for (int e = 0; e < 16; e++)
+                    lds[(wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * TP + wn * WN + j * 32 +
+                        (lane & 31)] = acc2[i][j][e];
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    lds[(wm * WM + i * 16 + 4 * (lane >> 4) + r) * TP + wn * WN + j * 16 + (lane & 15)] = acc[i][j][r];
+    }
     bar();
     if (g.splits > 1) {
         float *P = g.out + (zb * g.splits + slice) * (int64_t)g.m * g.n;

@@ -36,8 +36,6 @@ namespace {
 
 using namespace dma;
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 constexpr int XCDS = 8;
 constexpr int TN = 128;  // output tile columns (both shapes)
 
