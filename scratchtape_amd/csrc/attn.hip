@@ -71,14 +71,35 @@ __device__ __forceinline__ half8 ld_frag(const float *p) {
                  (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
 }
 
-// Shapes of a problem of T = 16 NB rows: NT threads (one wave per 16-row
-// block), LDS row pitch KP for row-major tiles and LDT for transposed ones
-// (8 halves of padding spread the rows over the LDS banks).
-template <int NB>
+// Shapes of a problem of T = 16 NB rows: G workgroups per problem (and
+// role) of W waves, one wave per 16-row block; LDS row pitch KP for row-major
+// tiles and LDT for transposed ones (8 halves of padding spread the rows over
+// the LDS banks).  With G = 2 the blocks pair as (p, NB - 1 - p), whose causal
+// work is NB + 1 tiles per pair, and workgroup x takes the pairs p = x, x + 2,
+// .., so both carry the same work and a problem spreads over two CUs.  The
+// forward splits (its 128 problems would fill half the CUs of the device);
+// the backward, with two roles per problem already, does not (four
+// workgroups per problem staging full panels measured slower).
+template <int NB, int G_>
 struct Split {
-    static constexpr int NT = 64 * NB;
+    static constexpr int G = G_;
+    static constexpr int W = G == 1 ? NB : 2 * ((NB + 3) / 4);
+    static constexpr int NT = 64 * W;
     static constexpr int T = NB * 16, KP = HD + 8, LDT = T + 8;
 };
+template <int NB>
+using SplitF = Split<NB, (NB >= 4 ? 2 : 1)>;
+template <int NB>
+using SplitB = Split<NB, 1>;
+
+// Block of wave w of workgroup x of a problem, or -1 (a wave without a block
+// when the pairs do not split evenly).
+template <int NB, int G>
+__device__ __forceinline__ int block_of(int w, int x) {
+    if constexpr (G == 1) return w;
+    const int p = 2 * (w >> 1) + x;
+    return p < NB / 2 ? ((w & 1) ? NB - 1 - p : p) : -1;
+}
 
 // Rows [0, n) (n % 32 == 0) of x (64 columns, row stride ld floats) into LDS
 // as f16: row-major xr[n][kp] and / or transposed xt[64][ldt].  Thread i
@@ -161,12 +182,12 @@ __device__ __forceinline__ bool unit_of(int U, int64_t nz, int64_t &z, int &u) {
     return z < nz;
 }
 
-// grid 8 ceil(B*H / 8) (unit_of, one workgroup per problem), NB waves per workgroup.
+// grid 8 G ceil(B*H / 8) (unit_of, G workgroups per problem), W waves per workgroup.
 template <int NB>
-__global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restrict__ qkv, float *__restrict__ ctx,
+__global__ __launch_bounds__(SplitF<NB>::NT) void k_attn_fwd(const float *__restrict__ qkv, float *__restrict__ ctx,
                                                             float *__restrict__ lse, int32_t h, int64_t nz,
                                                             float scale, int32_t one) {
-    using S = Split<NB>;
+    using S = SplitF<NB>;
     constexpr int T = S::T, KP = S::KP, LDT = S::LDT;
     const float sl2 = scale * LOG2E;
     __shared__ _Float16 sK[T * KP];
@@ -174,19 +195,21 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restr
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
     int64_t z;
     int x;
-    if (!unit_of(1, nz, z, x)) return;
-    const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's block
+    if (!unit_of(S::G, nz, z, x)) return;
+    const int j = __builtin_amdgcn_readfirstlane(block_of<NB, S::G>(tid >> 6, x));  // this wave's block
+    const int jj = j < 0 ? 0 : j;  // a block whose rows exist, for the loads of a wave without one
     const int64_t bb = z / h;
     const int hh = (int)(z % h);
     const int64_t D = (int64_t)h * HD, ld = 3 * D;
     const float *base = qkv + bb * T * ld + hh * HD;  // + 0: Q, + D: K, + 2D: V
 
     // This wave's query fragments (B operands) first, so their loads overlap the staging.
-    const float *qrow = base + (int64_t)(16 * j + li) * ld;
+    const float *qrow = base + (int64_t)(16 * jj + li) * ld;
     const half8 q0 = ld_frag(qrow + 8 * g), q1 = ld_frag(qrow + 32 + 8 * g);
     stage<S::NT, T>(base + D, ld, T, sK, KP, nullptr, 0, tid);
     stage<S::NT, T>(base + 2 * D, ld, T, nullptr, 0, sVt, LDT, tid);
     __syncthreads();
+    if (j < 0) return;
 
     {
         const int qb = j;
@@ -278,15 +301,15 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_fwd(const float *__restr
     }
 }
 
-// grid 16 ceil(B*H / 8) (unit_of, two workgroups per problem: one computing
-// dK, dV by key block, one computing dQ by query block), NB waves per workgroup.
+// grid 16 G ceil(B*H / 8) (unit_of, 2 G workgroups per problem: G computing
+// dK, dV by key block, G computing dQ by query block), W waves per workgroup.
 template <int NB>
-__global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restrict__ qkv,
+__global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__restrict__ qkv,
                                                             const float *__restrict__ ctx,
                                                             const float *__restrict__ dctx,
                                                             const float *__restrict__ lse, float *__restrict__ dqkv,
                                                             int32_t h, int64_t nz, float scale) {
-    using S = Split<NB>;
+    using S = SplitB<NB>;
     constexpr int T = S::T, KP = S::KP, LDT = S::LDT;
     const float sl2 = scale * LOG2E;
     // dK/dV units: Q, dO row-major, Q^T, dO^T; dQ units: K, V row-major, K^T.
@@ -296,9 +319,10 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
     int64_t z;
     int x;
-    if (!unit_of(2, nz, z, x)) return;
-    const bool kv = x == 0;
-    const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's block
+    if (!unit_of(2 * S::G, nz, z, x)) return;
+    const bool kv = x < S::G;
+    const int j = __builtin_amdgcn_readfirstlane(block_of<NB, S::G>(tid >> 6, kv ? x : x - S::G));  // this wave's block
+    const int jj = j < 0 ? 0 : j;  // a block whose rows exist, for the loads of a wave without one
     const int64_t bb = z / h;
     const int hh = (int)(z % h);
     const int64_t D = (int64_t)h * HD, ld = 3 * D;
@@ -310,7 +334,7 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
 
     if (kv) {
         // This wave's key and value fragments (B operands) first.
-        const float *krow = base + D + (int64_t)(16 * j + li) * ld, *vrow = krow + D;
+        const float *krow = base + D + (int64_t)(16 * jj + li) * ld, *vrow = krow + D;
         const half8 k0 = ld_frag(krow + 8 * g), k1 = ld_frag(krow + 32 + 8 * g);
         const half8 v0 = ld_frag(vrow + 8 * g), v1 = ld_frag(vrow + 32 + 8 * g);
         // Q, dO (row-major and transposed), L and D = rowsum(dO o O) of every query.
@@ -318,6 +342,7 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
         stage<S::NT, T>(dobase, D, T, sR1, KP, sT1, LDT, tid, obase, D, sD);
         for (int r = tid; r < T; r += S::NT) sL[r] = lrow[r] * LOG2E;
         __syncthreads();
+        if (j < 0) return;
         {
             const int kb = j;
             const int key = 16 * kb + li;  // this lane's key
@@ -368,7 +393,7 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
         half8 q0, q1, d0, d1;
         float dsum = 0.f, L;
         {
-            const int64_t q = 16 * j + li;
+            const int64_t q = 16 * jj + li;
             const float *qr = base + q * ld, *dr = dobase + q * D, *orr = obase + q * D;
             float4 dv[4], ov[4];
 #pragma unroll
@@ -394,6 +419,7 @@ __global__ __launch_bounds__(Split<NB>::NT) void k_attn_bwd(const float *__restr
         stage<S::NT, T>(base + D, ld, T, sR0, KP, sT0, LDT, tid);
         stage<S::NT, T>(base + 2 * D, ld, T, sR1, KP, nullptr, 0, tid);
         __syncthreads();
+        if (j < 0) return;
         {
             const int qb = j;
             const int q = 16 * qb + li;  // this lane's query
@@ -438,7 +464,7 @@ template <int NB>
 void launch_fwd(const float *qkv, float *ctx, float *lse, int64_t b, int64_t h, float scale, int32_t one,
                 hipStream_t s) {
     const int64_t nz = b * h;
-    hipLaunchKernelGGL(k_attn_fwd<NB>, dim3((unsigned)(8 * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0, s,
+    hipLaunchKernelGGL(k_attn_fwd<NB>, dim3((unsigned)(8 * SplitF<NB>::G * ((nz + 7) / 8))), dim3(SplitF<NB>::NT), 0, s,
                        qkv, ctx, lse, (int32_t)h, nz, scale, one);
 }
 
@@ -446,7 +472,7 @@ template <int NB>
 void launch_bwd(const float *qkv, const float *ctx, const float *dctx, const float *lse, float *dqkv, int64_t b,
                 int64_t h, float scale, hipStream_t s) {
     const int64_t nz = b * h;
-    hipLaunchKernelGGL(k_attn_bwd<NB>, dim3((unsigned)(16 * ((nz + 7) / 8))), dim3(Split<NB>::NT), 0,
+    hipLaunchKernelGGL(k_attn_bwd<NB>, dim3((unsigned)(16 * SplitB<NB>::G * ((nz + 7) / 8))), dim3(SplitB<NB>::NT), 0,
                        s, qkv, ctx, dctx, lse, dqkv, (int32_t)h, nz, scale);
 }
 
