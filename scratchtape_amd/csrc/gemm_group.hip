@@ -86,6 +86,7 @@ struct GroupArgs {
     uint8_t owner[XCDS][SCHED_MAX];
 };
 static_assert(sizeof(GroupArgs) <= 4000, "kernel arguments");
+static_assert(sizeof(GroupArgs) % 4 == 0, "copied to LDS as 32-bit words");
 
 // A unit of work of one workgroup: one output tile (or split slice) of one GEMM.
 template <class C>
@@ -449,6 +450,7 @@ struct SumArgs {
     SProb p[st::GROUP_MAX];
     int32_t count;
 };
+static_assert(sizeof(SumArgs) % 4 == 0, "copied to LDS as 32-bit words");
 
 // The split GEMMs' partial sums, one thread per 4 outputs (then one per
 // column sum), as k_sum_slices; thread ranges per GEMM start at t0.  The
