@@ -132,11 +132,12 @@ def time_events(fn, reps, stream):
     return s.elapsed_time(e) / reps
 
 
-def time_graph_steps(fn, steps, stream, reps=5, spread=None):
+def time_graph_steps(fn, steps, stream, reps=5, spread=None, warm_s=0.025):
     """The K timed steps captured as ONE HIP graph (each step's calls in full, in order): ms per step, without the
-    launch overhead a separate graph per step pays (several us each).  The graph is replayed `reps` times, each
-    replay (exactly K steps) timed on its own between HIP events; the median replay is reported (min and max go
-    into `spread` when given)."""
+    launch overhead a separate graph per step pays (several us each).  The graph is first replayed untimed for
+    about `warm_s` seconds (the device settles at its sustained clocks: the first replays of a cold process read a
+    few percent slower), then `reps` times, each replay (exactly K steps) timed on its own between HIP events; the
+    median replay is reported (min, max and the untimed replays go into `spread` when given)."""
     import torch
     fn()
     torch.cuda.synchronize()
@@ -144,12 +145,15 @@ def time_graph_steps(fn, steps, stream, reps=5, spread=None):
     with torch.cuda.graph(g, stream=stream):
         for _ in range(steps):
             fn()
-    g.replay()  # untimed: the graph's first replay
-    torch.cuda.synchronize()
+    warm, t0 = 0, time.perf_counter()
+    while warm < 200 and (warm < 1 or time.perf_counter() - t0 < warm_s):
+        g.replay()
+        torch.cuda.synchronize()
+        warm += 1
     per = sorted(time_events(g.replay, 1, stream) / steps for _ in range(reps))
     del g
     if spread is not None:
-        spread.update(min_ms=round(per[0], 5), max_ms=round(per[-1], 5), replays=reps)
+        spread.update(min_ms=round(per[0], 5), max_ms=round(per[-1], 5), replays=reps, untimed_replays=warm)
     return per[len(per) // 2]
 
 
