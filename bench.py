@@ -692,8 +692,8 @@ def main():
         print(json.dumps({"calib_copy_bytes_each_way": src.numel() * 4, "dispatches": 10}))
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs on a single MI355X (asked for --gpus {args.gpus}); "
-              "see the sharding design for more than one", file=sys.stderr)
+        print(f"bench.py measures one GPU: the library runs on a single MI355X (asked for --gpus {args.gpus}); "
+              "how the path would shard over more is a design note, not a measured run", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,7 +1,7 @@
 """CPU oracle for the scratchtape matrix-multiplication hot path.
 
-TEST INFRASTRUCTURE ONLY: the checker used by ``tests/``, by the package
-``__graft_entry__.smoke()`` and by ``bench.py``'s CPU baseline.  The product
+TEST INFRASTRUCTURE ONLY: what ``tests/`` and the package ``__graft_entry__.smoke()``
+compare the library against, and ``bench.py``'s CPU baseline.  The product
 library (``scratchtape_amd``) never imports this module.
 
 The arithmetic lives in ``oracle.c`` (built to ``liboracle.so`` by the Makefile

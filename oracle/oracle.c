@@ -2,9 +2,9 @@
  * CPU oracle for the scratchtape matrix-multiplication hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  This file restates, in plain C, the reference
- * algorithms the HIP library must reproduce.  It is the checker for the
- * parity tests, the small-case check inside the package smoke run and the
- * CPU baseline timed by the benchmark.  Nothing in the product library links,
+ * algorithms the HIP library must reproduce.  The parity tests and the
+ * small-case check inside the package smoke run compare the library against
+ * it, and the benchmark times it as the CPU baseline.  Nothing in the product library links,
  * loads or calls it.
  *
  * Build: gcc -O3 -mavx2 -mfma -ffp-contract=off -fopenmp -fPIC -shared (see

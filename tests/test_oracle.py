@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the parity tests rely on it.
 
 Each check is chosen so that a plausible mistake in the restatement (a wrong
 shift or constant, FMA contraction, a wrong index, a transposed operand, a
