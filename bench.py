@@ -517,11 +517,21 @@ class KnnBench:
                 self.search(i)
             e.record(stream)
             e.synchronize()
-            ms = s.elapsed_time(e) / steps
+            eager_ms = s.elapsed_time(e) / steps
+            # The same K searches (batches 0 .. K-1) captured as one HIP graph, as the GEMM lines are timed.
+            used, it = [], itertools.count()
+
+            def one():
+                i = next(it)
+                used.append(i)
+                self.search(i)
+            spread = {}
+            ms = time_graph_steps(one, steps, stream, spread=spread)
         nb = len(self.batches)
-        pairs = np.mean([self.batches[i % nb]["pairs"] for i in range(steps)])
-        byts = np.mean([self.batches[i % nb]["bytes"] for i in range(steps)])
-        return ms, pairs, byts
+        used = used[1:1 + steps]  # the call before the capture is not in the graph
+        pairs = np.mean([self.batches[i % nb]["pairs"] for i in used])
+        byts = np.mean([self.batches[i % nb]["bytes"] for i in used])
+        return ms, pairs, byts, dict(eager_ms=round(eager_ms, 5), graph_spread=spread)
 
     def check(self, qis=(0, 100, 255)):
         """Bit-exact top-128 for a few queries of batch 0 against the oracle over the same stored bytes."""
@@ -616,7 +626,10 @@ class ProbeBench:
             for _ in range(warmup):
                 self.probe(next(it))
             torch.cuda.synchronize()
-            return time_events(lambda: self.probe(next(it)), steps, stream)
+            eager_ms = time_events(lambda: self.probe(next(it)), steps, stream)
+            spread = {}
+            ms = time_graph_steps(lambda: self.probe(next(it)), steps, stream, spread=spread)
+        return ms, dict(eager_ms=round(eager_ms, 5), graph_spread=spread)
 
     def check(self):
         import oracle
@@ -769,9 +782,9 @@ def main():
         if not ok:
             log("[bench] PARITY FAILURE: refusing to report")
             sys.exit(3)
-        ms, pairs, byts = kb.run(stream, args.steps, args.warmup)
+        ms, pairs, byts, timing = kb.run(stream, args.steps, args.warmup)
         gbs = byts / ms / 1e6
-        knn = dict(ms_per_batch=round(ms, 5), keys_per_s=round(pairs / ms * 1e3, 1),
+        knn = dict(ms_per_batch=round(ms, 5), **timing, keys_per_s=round(pairs / ms * 1e3, 1),
                    g_keys_per_s=round(pairs / ms / 1e6, 3), pairs_per_batch=int(pairs),
                    distinct_cell_bytes=int(byts), hbm_gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK["hbm_gbs"], 4),
                    roofline=dict(kernel="k_search (st_knn_search_ivf_2bit: one fused launch)", bound="hbm",
@@ -790,8 +803,8 @@ def main():
         if not pok:
             log("[bench] PARITY FAILURE: refusing to report")
             sys.exit(3)
-        pms = pb.run(stream, args.steps, args.warmup)
-        probe = dict(ms_per_batch=round(pms, 5), queries_per_s=round(pb.NQ / pms * 1e3, 1),
+        pms, ptiming = pb.run(stream, args.steps, args.warmup)
+        probe = dict(ms_per_batch=round(pms, 5), **ptiming, queries_per_s=round(pb.NQ / pms * 1e3, 1),
                      roofline=roofline("st_knn_probe (k_probe_prep + k_probe_dots + k_probe_select)", pb.ops,
                                        pb.bytes, pms,
                                        traffic_for("st_knn_probe", "scratchtape_amd/csrc/knn_probe.hip"), route="i8"))
@@ -813,9 +826,12 @@ def main():
             def masked():
                 i = next(it)
                 kb.store.search_masked(kb.batches[i % 8]["q"], lohis[i % 8], 0, 128, out=kb.out)
-            mms = time_events(masked, args.steps, stream)
+            meager = time_events(masked, args.steps, stream)
+            mspread = {}
+            mms = time_graph_steps(masked, args.steps, stream, spread=mspread)
         mbytes = kb.NQ * 81920 * (kb.D // 4 + 4)
-        extra["c5_knn_masked"] = dict(ms_per_batch=round(mms, 5), g_keys_per_s=round(kb.NQ * 81920 / mms / 1e6, 3),
+        extra["c5_knn_masked"] = dict(ms_per_batch=round(mms, 5), eager_ms=round(meager, 5), graph_spread=mspread,
+                                      g_keys_per_s=round(kb.NQ * 81920 / mms / 1e6, 3),
                                       roofline=dict(kernel="k_search<MASKED> (st_knn_search_masked_2bit)", bound="hbm",
                                                     achieved=round(mbytes / mms / 1e6, 1), peak=PEAK["hbm_gbs"],
                                                     unit="GB/s", frac=round(mbytes / mms / 1e6 / PEAK["hbm_gbs"], 4),
@@ -828,8 +844,8 @@ def main():
                 kb.store.search_ivf(kb.batches[i % 8]["q"], 8, 128, out=kb.out)
             torch.cuda.synchronize()
             it = itertools.count()
-            e2e = time_events(lambda: kb.store.search_ivf(kb.batches[next(it) % 8]["q"], 8, 128, out=kb.out),
-                              args.steps, stream)
+            e2e = time_graph_steps(lambda: kb.store.search_ivf(kb.batches[next(it) % 8]["q"], 8, 128, out=kb.out),
+                                   args.steps, stream)
         probe["search_ivf_by_nprobe_ms_per_batch"] = round(e2e, 5)
         extra["c5_knn_probe"] = probe
         del pb

@@ -2,11 +2,12 @@
 the program's own eager work and synchronisations in between, and every replay must give the eager results bit for
 bit (the same kernels on the same inputs are deterministic).  Nothing here records a memset into a graph: the
 grouped GEMM's split-k sums, the row kernels' partials and every clear are kernels."""
+import numpy as np
 import pytest
 import torch
 
 import scratchtape_amd as st
-from scratchtape_amd import MatRef, attention, rows
+from scratchtape_amd import MatRef, attention, knn, rows
 
 pytestmark = pytest.mark.gpu
 
@@ -14,7 +15,8 @@ REPLAYS = 3
 
 
 def replay_and_check(fn, outputs, reset=None):
-    """Eager run -> reference copies; then a graph of two calls of fn, replayed REPLAYS times."""
+    """Eager run -> reference copies; then a graph of two calls of fn, replayed REPLAYS times (stale outputs
+    cannot pass: they are overwritten with NaN, or -7 for integers, before each replay)."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         if reset:
@@ -33,7 +35,7 @@ def replay_and_check(fn, outputs, reset=None):
         junk = torch.randn(1 << 20, device="cuda")
         for r in range(REPLAYS):
             for o in outputs:
-                o.fill_(float("nan"))       # eager work between replays; stale outputs cannot pass
+                o.fill_(float("nan") if o.is_floating_point() else -7)  # eager work between replays
             junk.mul_(1.0001).add_(0.5)
             torch.cuda.synchronize()
             g.replay()
@@ -91,3 +93,26 @@ def test_layer_norm_step_replays_from_a_graph(dev):
     step()
     torch.cuda.synchronize()
     replay_and_check(step, [dx, grads], reset=grads.zero_)
+
+
+def test_knn_search_probe_and_masked_search_replay_from_a_graph(dev):
+    """The benchmark's kNN lines: probe selection, the IVF scan and the masked scan, one graph."""
+    rng = np.random.default_rng(17)
+    sizes = rng.integers(200, 900, 48)
+    cell_start = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    keys = torch.from_numpy(rng.standard_normal((int(cell_start[-1]), 256)).astype(np.float32)).to(dev)
+    store = knn.KnnStore2bit.from_keys(keys, cell_start)
+    store.set_centroids(torch.from_numpy(rng.standard_normal((48, 256)).astype(np.float32)).to(dev))
+    nq = 24
+    q = torch.from_numpy(rng.standard_normal((nq, 256)).astype(np.float32)).to(dev)
+    probes = torch.empty((nq, 6), dtype=torch.int32, device=dev)
+    lo = rng.integers(0, int(cell_start[-1]) - 3000, nq)
+    lohi = torch.from_numpy(np.stack([lo, lo + 3000], 1).astype(np.int64)).to(dev)
+    ivf = (torch.empty((nq, 128), dtype=torch.int64, device=dev), torch.empty((nq, 128), device=dev))
+    msk = (torch.empty((nq, 128), dtype=torch.int64, device=dev), torch.empty((nq, 128), device=dev))
+
+    def step():
+        store.centroids.probe(q, 6, out=probes)
+        store.search_ivf(q, probes, 128, out=ivf)
+        store.search_masked(q, lohi, 500, 128, out=msk)
+    replay_and_check(step, [probes, *ivf, *msk])
