@@ -655,7 +655,8 @@ class ProbeBench:
 
 def device_ceilings(dev, stream):
     """Measured ceilings beside the published peaks every roofline is priced against: the matrix cores with only
-    independent MFMA chains in flight (two waves per SIMD, 8 chains each), a plain streaming read of 1 GiB, and the
+    independent MFMA chains in flight (two waves per SIMD, 8 chains each), a streaming read of 1 GiB (one workgroup of 16
+    waves per CU, each reading its own slab with eight 16-byte loads per lane in flight, as the key scans read), and the
     device's CU count and clocks (HIP device attributes)."""
     import ctypes
     import torch
@@ -673,7 +674,7 @@ def device_ceilings(dev, stream):
             ms = time_events(f, 5, stream)
             out[f"mfma_{name}_tflops_measured"] = round(blocks * waves * chains * iters * per / ms / 1e9, 1)
         buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-        g = lambda: _lib.call("st_peak_read", buf.data_ptr(), buf.numel() * 4, 8 * cus, sink.data_ptr(),
+        g = lambda: _lib.call("st_peak_read", buf.data_ptr(), buf.numel() * 4, cus, sink.data_ptr(),
                               stream.cuda_stream)
         g()
         ms = time_events(g, 10, stream)

@@ -1,7 +1,7 @@
 // Device ceilings for the benchmark's roofline context (no reference
 // counterpart, on no data path): the matrix cores' throughput with nothing but
 // independent MFMA chains in flight, the HBM read rate of a plain streaming
-// kernel, and the device's CU count and clocks.  The benchmark reports these
+// kernel in the key scans' launch shape, and the device's CU count and clocks.  The benchmark reports these
 // beside the published peaks it prices every kernel against.
 #include "common.h"
 
@@ -59,17 +59,30 @@ __global__ __launch_bounds__(256) void k_peak_mfma(int64_t iters, float *__restr
     if (s == NEVER) sink[blockIdx.x] = s;
 }
 
-// Reads src [n4] float4 once (grid-stride, four loads in flight per thread).
-__global__ __launch_bounds__(256) void k_peak_read(const float4 *__restrict__ src, int64_t n4,
-                                                   float *__restrict__ sink) {
-    const int64_t stride = (int64_t)gridDim.x * 256;
+// Reads src [n4] float4 once, in the shape the key scans stream their bytes:
+// workgroup b reads its own contiguous slab (whole 1 KB blocks), its 16 waves
+// taking the slab's 1 KB blocks in turn, each lane with eight 16-byte loads in
+// flight.
+constexpr int RT = 1024;      // threads per workgroup
+constexpr int RDEPTH = 8;     // loads in flight per lane
+__global__ __launch_bounds__(RT) void k_peak_read(const float4 *__restrict__ src, int64_t n4,
+                                                  float *__restrict__ sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t per = ((n4 + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
+    const int64_t s0 = (int64_t)blockIdx.x * per;
+    const int64_t s1 = s0 + per < n4 ? s0 + per : n4;
+    constexpr int64_t STEP = (int64_t)RDEPTH * (RT / 64) * 64;
     float acc = 0.f;
-    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    for (; i + 3 * stride < n4; i += 4 * stride) {
-        const float4 v0 = src[i], v1 = src[i + stride], v2 = src[i + 2 * stride], v3 = src[i + 3 * stride];
-        acc += (v0.x + v1.y) + (v2.z + v3.w);
+    for (int64_t b = s0 + (int64_t)wave * 64 + lane; b < s1; b += STEP) {
+        float4 v[RDEPTH];
+#pragma unroll
+        for (int d = 0; d < RDEPTH; d++) {
+            const int64_t e = b + (int64_t)d * (RT / 64) * 64;
+            v[d] = e < s1 ? src[e] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int d = 0; d < RDEPTH; d++) acc += v[d].x + v[d].w;
     }
-    for (; i < n4; i += stride) acc += src[i].x;
     if (acc == NEVER) sink[blockIdx.x] = acc;
 }
 
@@ -105,7 +118,7 @@ extern "C" st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks
     if (!src || !sink || bytes < 16 || bytes % 16 || blocks < 1 || (reinterpret_cast<uintptr_t>(src) & 15))
         return st::fail(ST_ERR_INVALID, "peak_read: need a 16-byte aligned buffer of a multiple of 16 bytes");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
-    hipLaunchKernelGGL(k_peak_read, dim3((unsigned)blocks), dim3(256), 0, st::stream_of(stream),
+    hipLaunchKernelGGL(k_peak_read, dim3((unsigned)blocks), dim3(RT), 0, st::stream_of(stream),
                        reinterpret_cast<const float4 *>(src), bytes / 16, sink);
     ST_LAUNCH_CHECK();
     return ST_OK;
