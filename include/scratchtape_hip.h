@@ -7,9 +7,14 @@
  *  - Device buffers are plain device pointers (the reference's cubecl
  *    `Handle`s).  The caller owns every operand and output; outputs are
  *    written in place.  The library owns only a grow-only scratch arena per
- *    device (split-k partials), like the reference's `split_scratch`
+ *    device and use (split-k partials, probe-selection distances, LayerNorm
+ *    column partials), like the reference's `split_scratch`
  *    (gpu_step/matmul.rs:207-217); the kNN search keeps its candidate lists
- *    in LDS and allocates nothing.
+ *    in LDS and allocates nothing.  An arena grows only outside graph
+ *    capture: a call that would grow it while its stream is being captured
+ *    fails with ST_ERR_INVALID (run the call once before capturing).  A
+ *    superseded arena buffer is kept, not freed, until st_scratch_release(),
+ *    so a graph captured earlier never replays into freed memory.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL is the default
  *    stream) and is asynchronous, as the reference's single in-order queue
  *    (gpu_step/mod.rs:42, 78).  Calls that use the scratch arena (split-k
@@ -126,7 +131,8 @@ int32_t st_f16_enabled(void);
 
 /* src/tensor.rs:241 `NdArray::matmul` on host buffers: out[m, n] = a[m, k] @
  * b[k, n], row-major f32, computed on the GPU in f32 (host buffers in and out;
- * synchronous).  Thread-safe. */
+ * synchronous).  Thread-safe: each call has its own stream and its own
+ * split-k scratch (allocated and freed inside the call). */
 st_status st_ndarray_matmul(const float *a, const float *b, float *out, int64_t m, int64_t k,
                             int64_t n);
 
@@ -280,7 +286,8 @@ st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *mem_clock_kh
 
 /* `blocks` workgroups of 4 waves, each wave running 8 independent MFMA chains
  * of `iters` steps: kind 0 v_mfma_f32_16x16x32_f16 (16384 FLOP per step),
- * 1 v_mfma_f32_16x16x4_f32 (2048), 2 v_mfma_i32_16x16x64_i8 (32768 OP).
+ * 1 v_mfma_f32_16x16x4_f32 (2048), 2 v_mfma_i32_16x16x64_i8 (32768 OP),
+ * 3 v_mfma_f32_32x32x16_f16 (32768), 4 v_mfma_i32_32x32x32_i8 (65536 OP).
  * The caller times it; `sink` ([blocks] floats) is never written in practice
  * (a guarded store keeps the chains live). */
 st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink, st_stream stream);
@@ -294,6 +301,13 @@ st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks, float *si
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *st_last_error(void);
+
+/* No reference counterpart (the reference's cubecl client owns its memory
+ * until exit): waits for every device the library used, then frees all of its
+ * scratch arenas, current and superseded.  Only for callers that will not
+ * replay again any graph that captured a library call; the next call that
+ * needs scratch allocates it anew. */
+st_status st_scratch_release(void);
 
 /* Waits for the work enqueued on `stream`. */
 st_status st_sync(st_stream stream);

@@ -80,6 +80,7 @@ SIGNATURES = {
     "st_peak_read": [_vp, _i64, _i32, _vp, _vp],
     "st_last_error": [],
     "st_sync": [_vp],
+    "st_scratch_release": [],
     "st_version": [],
 }
 _RESTYPES = {"st_last_error": ctypes.c_char_p, "st_version": ctypes.c_char_p, "st_f16_enabled": _i32,

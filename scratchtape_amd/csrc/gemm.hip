@@ -539,8 +539,8 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
     if (splits > 1) {
         const size_t base = (size_t)(batch * splits * m * n);
         const size_t extra = epi.has_col_sum ? (size_t)(batch * splits * n) : 0;
-        partial = static_cast<float *>(st::scratch(st::SCRATCH_SPLITK, (base + extra) * sizeof(float)));
-        if (!partial) return ST_ERR_OOM;
+        partial = static_cast<float *>(st::scratch(st::SCRATCH_SPLITK, (base + extra) * sizeof(float), stream));
+        if (!partial) return st::scratch_status();
         g.out = partial;
         g.o_stride = m * n;
         g.o_group = 1;
@@ -681,6 +681,9 @@ extern "C" st_status st_ndarray_matmul(const float *a, const float *b, float *ou
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     hipStream_t s;
     ST_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    // Split-k partials in buffers of this call's own (freed when it returns):
+    // concurrent calls never share the library's arena.
+    st::ScratchScope private_scratch;
     float *da = nullptr, *db = nullptr, *dc = nullptr;
     st_status rc = ST_OK;
     const size_t ba = sizeof(float) * (size_t)(m * k), bb = sizeof(float) * (size_t)(k * n),

@@ -388,9 +388,9 @@ bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
     if (splits > 1) {
         const size_t pfl = (size_t)(batch * splits * m * n);
         const size_t cfl = d.has_cs ? (size_t)(batch * splits * n) : 0;
-        part = static_cast<float *>(scratch(SCRATCH_SPLITK, sizeof(float) * (pfl + cfl)));
+        part = static_cast<float *>(scratch(SCRATCH_SPLITK, sizeof(float) * (pfl + cfl), stream));
         if (!part) {
-            *status = ST_ERR_OOM;
+            *status = scratch_status();
             return true;
         }
         cs_part = part + pfl;

@@ -640,8 +640,8 @@ st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_
     }
     float *part = nullptr;
     if (part_floats) {
-        part = static_cast<float *>(st::scratch(st::SCRATCH_SPLITK, part_floats * sizeof(float)));
-        if (!part) return ST_ERR_OOM;
+        part = static_cast<float *>(st::scratch(st::SCRATCH_SPLITK, part_floats * sizeof(float), stream));
+        if (!part) return st::scratch_status();
     }
 
     GroupArgs ga;

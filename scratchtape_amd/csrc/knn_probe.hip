@@ -472,8 +472,8 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
     if (chunk > nq) chunk = cdiv(nq, BLK) * BLK;
     const int64_t dd_bytes = chunk * nlist * (int64_t)sizeof(double);
     const int64_t dig_bytes = cdiv(chunk, BLK) * BLK_BYTES;
-    char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, (size_t)(dd_bytes + dig_bytes + chunk * 4)));
-    if (!base) return ST_ERR_OOM;
+    char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, (size_t)(dd_bytes + dig_bytes + chunk * 4), s));
+    if (!base) return st::scratch_status();
     double *dd = reinterpret_cast<double *>(base);
     int8_t *qdig = reinterpret_cast<int8_t *>(base + dd_bytes);
     int32_t *qex = reinterpret_cast<int32_t *>(base + dd_bytes + dig_bytes);

@@ -10,6 +10,8 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
 
 constexpr int CHAINS = 8;  // independent accumulators per wave (covers the MFMA latency)
 
@@ -18,7 +20,8 @@ constexpr int CHAINS = 8;  // independent accumulators per wave (covers the MFMA
 constexpr float NEVER = -1.2345e30f;
 
 // kind 0: v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x4_f32,
-// 2: v_mfma_i32_16x16x64_i8.  Operands come from the lane id so that nothing
+// 2: v_mfma_i32_16x16x64_i8, 3: v_mfma_f32_32x32x16_f16 (the GEMMs' form),
+// 4: v_mfma_i32_32x32x32_i8.  Operands come from the lane id so that nothing
 // folds; magnitudes stay small, so no accumulator overflows or turns inf.
 template <int KIND>
 __global__ __launch_bounds__(256) void k_peak_mfma(int64_t iters, float *__restrict__ sink) {
@@ -46,6 +49,30 @@ __global__ __launch_bounds__(256) void k_peak_mfma(int64_t iters, float *__restr
             for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[c], 0, 0, 0);
         }
         for (int c = 0; c < CHAINS; c++) s += acc[c][0] + acc[c][3];
+    } else if constexpr (KIND == 3) {
+        half8 a, b;
+        for (int e = 0; e < 8; e++) {
+            a[e] = (_Float16)(1e-3f * (float)((lane + e) & 7));
+            b[e] = (_Float16)(1e-3f * (float)((lane * 3 + e) & 7));
+        }
+        f32x16 acc[CHAINS];
+        for (int c = 0; c < CHAINS; c++)
+            for (int e = 0; e < 16; e++) acc[c][e] = 0.f;
+        for (int64_t i = 0; i < iters; i++) {
+#pragma unroll
+            for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+        }
+        for (int c = 0; c < CHAINS; c++) s += acc[c][0] + acc[c][15];
+    } else if constexpr (KIND == 4) {
+        const v4i a = {lane & 1, (lane >> 1) & 1, 0, 1}, b = {1, 0, lane & 1, 0};
+        v16i acc[CHAINS];
+        for (int c = 0; c < CHAINS; c++)
+            for (int e = 0; e < 16; e++) acc[c][e] = 0;
+        for (int64_t i = 0; i < iters; i++) {
+#pragma unroll
+            for (int c = 0; c < CHAINS; c++) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
+        }
+        for (int c = 0; c < CHAINS; c++) s += (float)(acc[c][0] + acc[c][15]);
     } else {
         const v4i a = {lane & 1, (lane >> 1) & 1, 0, 1}, b = {1, 0, lane & 1, 0};
         v4i acc[CHAINS];
@@ -104,10 +131,15 @@ extern "C" st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *m
 
 extern "C" st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink, st_stream stream) {
     st::clear_error();
-    if (kind < 0 || kind > 2) return st::fail(ST_ERR_INVALID, "peak_mfma: kind is 0 (f16), 1 (f32) or 2 (i8)");
+    if (kind < 0 || kind > 4)
+        return st::fail(ST_ERR_INVALID,
+                        "peak_mfma: kind is 0 (f16 16x16x32), 1 (f32), 2 (i8 16x16x64), 3 (f16 32x32x16) or 4 (i8 "
+                        "32x32x32)");
     if (iters < 1 || blocks < 1 || !sink) return st::fail(ST_ERR_INVALID, "peak_mfma: bad iters, blocks or sink");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
-    void (*k)(int64_t, float *) = kind == 0 ? k_peak_mfma<0> : kind == 1 ? k_peak_mfma<1> : k_peak_mfma<2>;
+    void (*const kernels[])(int64_t, float *) = {k_peak_mfma<0>, k_peak_mfma<1>, k_peak_mfma<2>, k_peak_mfma<3>,
+                                                  k_peak_mfma<4>};
+    void (*k)(int64_t, float *) = kernels[kind];
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st::stream_of(stream), iters, sink);
     ST_LAUNCH_CHECK();
     return ST_OK;

@@ -264,8 +264,8 @@ extern "C" st_status st_layer_norm_backward(const float *dy, const float *x, con
     const int64_t rows_pm = rows / models, nch = (rows_pm + LN_CHUNK - 1) / LN_CHUNK;
     if (nch > 65535 || models > 65535 || (d + 63) / 64 > INT32_MAX)
         return st::fail(ST_ERR_INVALID, "layer_norm_backward: too many rows per model or models");
-    float *part = static_cast<float *>(st::scratch(st::SCRATCH_ROWS, (size_t)(models * nch * 2 * d) * sizeof(float)));
-    if (!part) return ST_ERR_OOM;
+    float *part = static_cast<float *>(st::scratch(st::SCRATCH_ROWS, (size_t)(models * nch * 2 * d) * sizeof(float), s));
+    if (!part) return st::scratch_status();
     hipLaunchKernelGGL(k_ln_bwd_dx, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, dy, x, mean, rstd, rows, d,
                        params, off, dx, accumulate, rows_pm, model_stride);
     ST_LAUNCH_CHECK();

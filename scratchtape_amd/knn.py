@@ -98,6 +98,18 @@ class Centroids:
         return out
 
 
+def _check_out(out, nq: int, k: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """A caller-supplied (idx, dist) pair must hold nq x k results on the queries' device: the kernels write
+    exactly that many and trust the sizes."""
+    idx, dist = out
+    for t, name in ((idx, "idx"), (dist, "dist")):
+        if tuple(t.shape) != (nq, k):
+            raise ValueError(f"out {name} must be [{nq}, {k}], got {list(t.shape)}")
+        if t.device != device:
+            raise ValueError(f"out {name} is on {t.device}, the queries on {device}")
+    return idx, dist
+
+
 class KnnStore2bit:
     """A cell-contiguous 2-bit key store on the device.
 
@@ -159,7 +171,7 @@ class KnnStore2bit:
             idx = torch.empty((nq, k), dtype=torch.int64, device=queries.device)
             dist = torch.empty((nq, k), dtype=torch.float32, device=queries.device)
         else:
-            idx, dist = out
+            idx, dist = _check_out(out, nq, k, queries.device)
         _lib.call("st_knn_search_ivf_2bit", _dptr(self.codes, torch.uint8, "codes"),
                   _dptr(self.scales, torch.float32, "scales"), self.cell_start_dev.data_ptr(), self.ncells,
                   self.max_cell, _dptr(queries, torch.float32, "queries"), _dptr(probes, torch.int32, "probes"),
@@ -180,7 +192,7 @@ class KnnStore2bit:
             idx = torch.empty((nq, k), dtype=torch.int64, device=queries.device)
             dist = torch.empty((nq, k), dtype=torch.float32, device=queries.device)
         else:
-            idx, dist = out
+            idx, dist = _check_out(out, nq, k, queries.device)
         _lib.call("st_knn_search_masked_2bit", _dptr(self.codes, torch.uint8, "codes"),
                   _dptr(self.scales, torch.float32, "scales"), len(self), _dptr(queries, torch.float32, "queries"),
                   _dptr(lohi, torch.int64, "lohi"), always, nq, d, k, _dptr(idx, torch.int64, "idx"),

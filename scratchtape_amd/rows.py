@@ -10,9 +10,21 @@ from . import _lib
 from .matmul import _ptr, _stream
 
 
+def _check_rows_out(out: torch.Tensor | None, n: int, device, name: str) -> None:
+    """A caller-supplied output must hold every element the kernel writes (rows x n floats) on the input's
+    device."""
+    if out is None:
+        return
+    if out.numel() < n:
+        raise ValueError(f"{name}: out holds {out.numel()} elements, the call writes {n}")
+    if out.device != device:
+        raise ValueError(f"{name}: out is on {out.device}, the input on {device}")
+
+
 def softmax(x: torch.Tensor, rows: int, n: int, t: int, scale: float, causal: bool, one: bool,
             out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Row-wise softmax of scale*x over x [rows, n] (rows.rs:101-112); returns y."""
+    _check_rows_out(out, rows * n, x.device, "softmax")
     y = out if out is not None else torch.empty(rows * n, dtype=torch.float32, device=x.device)
     _lib.call("st_softmax", _ptr(x), _ptr(y), rows, n, t, float(scale), int(causal), int(one), _stream(stream))
     return y
@@ -21,6 +33,7 @@ def softmax(x: torch.Tensor, rows: int, n: int, t: int, scale: float, causal: bo
 def softmax_backward(dy: torch.Tensor, y: torch.Tensor, rows: int, n: int, scale: float,
                      out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """dx = scale * y * (dy - sum(dy * y)) per row (rows.rs:114-123); returns dx."""
+    _check_rows_out(out, rows * n, y.device, "softmax_backward")
     dx = out if out is not None else torch.empty(rows * n, dtype=torch.float32, device=y.device)
     _lib.call("st_softmax_backward", _ptr(dy), _ptr(y), _ptr(dx), rows, n, float(scale), _stream(stream))
     return dx

@@ -140,9 +140,41 @@ def test_masked_search_arguments_are_validated():
 def test_ceiling_probe_arguments_are_validated():
     L = scratchtape_amd.lib()
     fake = 1 << 20
-    assert L.st_peak_mfma(3, 10, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_peak_mfma(5, 10, 8, fake, None) == _lib.ST_ERR_INVALID
     assert b"kind" in L.st_last_error()
     assert L.st_peak_mfma(0, 0, 8, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_peak_read(fake, 24, 8, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_peak_read(fake + 4, 32, 8, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_device_info(None, None, None, None) == _lib.ST_ERR_INVALID
+
+
+def test_caller_outputs_are_size_checked_before_any_device_call():
+    """A caller-supplied out smaller than what the kernel writes is refused on the host (CPU tensors: the
+    check runs before the C ABI is reached)."""
+    import torch
+
+    from scratchtape_amd import rows
+    from scratchtape_amd.knn import KnnStore2bit
+
+    store = KnnStore2bit(torch.zeros((300, 64), dtype=torch.uint8), torch.ones(300), [0, 100, 300])
+    q = torch.zeros((3, 256))
+    probes = torch.zeros((3, 2), dtype=torch.int32)
+    good = (torch.empty((3, 128), dtype=torch.int64), torch.empty((3, 128)))
+    for bad in ((torch.empty((3, 127), dtype=torch.int64), good[1]), (good[0], torch.empty((2, 128))),
+                (good[0], torch.empty(3 * 128))):
+        with pytest.raises(ValueError, match="out"):
+            store.search_ivf(q, probes, out=bad)
+        with pytest.raises(ValueError, match="out"):
+            store.search_masked(q, torch.zeros((3, 2), dtype=torch.int64), out=bad)
+    x = torch.zeros(4 * 8)
+    with pytest.raises(ValueError, match="writes 32"):
+        rows.softmax(x, 4, 8, 8, 1.0, True, False, out=torch.empty(31))
+    with pytest.raises(ValueError, match="writes 32"):
+        rows.softmax_backward(x, x, 4, 8, 1.0, out=torch.empty(16))
+
+
+def test_scratch_release_without_arenas_is_a_no_op():
+    L = scratchtape_amd.lib()
+    if L.st_scratch_release() != _lib.ST_OK:
+        # No HIP device in this process: the call reports it instead of crashing.
+        assert L.st_last_error()

@@ -36,7 +36,17 @@ def test_traffic_is_quoted_only_for_the_profiled_source():
     assert bench.traffic_for("no such kernel", "scratchtape_amd/csrc/knn.hip") is None
 
 
-@pytest.mark.parametrize("flops, nbytes, bound", [(20937965568, 236716032, "hbm"), (1e12, 1e6, "mfma")])
+def test_step_set_prices_each_distinct_tensor_once():
+    """The set's algorithmic bytes count X, W, dY (read by two GEMMs each) and Y, dX, dW once: 157,810,688 B, not
+    the 236,716,032 B of summing every GEMM's operands."""
+    ss = bench.StepSet("cpu")
+    assert ss.flops == 20937965568
+    assert ss.bytes == 157810688 and ss.per_gemm_bytes == 236716032
+    r = bench.roofline("k", ss.flops, ss.bytes, 0.07)
+    assert r["bound"] == "hbm" and r["roof_tflops"] == pytest.approx(1061.4, abs=0.1)
+
+
+@pytest.mark.parametrize("flops, nbytes, bound", [(20937965568, 157810688, "hbm"), (1e12, 1e6, "mfma")])
 def test_roofline_picks_the_binding_roof(flops, nbytes, bound):
     r = bench.roofline("k", flops, nbytes, 0.1, traffic=123, route="f16")
     assert r["bound"] == bound and r["traffic"] == 123

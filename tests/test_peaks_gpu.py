@@ -18,7 +18,7 @@ def test_device_info_reports_the_gpu():
     assert clk > 0 and mclk > 0 and bus > 0
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4])
 def test_mfma_probe_runs_and_leaves_the_sink(kind):
     sink = torch.zeros(64, device="cuda")
     s = torch.cuda.current_stream()
