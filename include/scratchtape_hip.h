@@ -125,6 +125,19 @@ typedef struct st_gemm {
  * scratch arena: serialise on one stream per device. */
 st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_stream stream);
 
+/* Size of the fixed device scratch of st_matmul_grouped_noalloc. */
+#define ST_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference: st_matmul_grouped for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results; the
+ * split-k partials live in a fixed per-device array of
+ * ST_NOALLOC_SCRATCH_BYTES instead of the library's arena, and the call
+ * allocates and frees nothing.  A group whose partials need more is refused
+ * with ST_ERR_INVALID.  Every call on a device shares that device's array:
+ * calls that overlap on one device race. */
+st_status st_matmul_grouped_noalloc(const st_gemm *gemms, int64_t count, st_stream stream);
+
 /* gpu_step/matmul.rs:97-102 `f16_enabled`: 1 unless the environment sets
  * TRAIN_F16=0 (gfx950 always has f16 x f16 -> f32 matrix cores).  Read once. */
 int32_t st_f16_enabled(void);

@@ -58,6 +58,7 @@ SIGNATURES = {
     "st_matmul_f32": [_R, _R, _R, _i64, _i64, _i64, _i64, _E, _vp],
     "st_matmul_with": [_R, _R, _R, _i64, _i64, _i64, _i64, _E, _i32, _vp],
     "st_matmul_grouped": [ctypes.POINTER(StGemm), _i64, _vp],
+    "st_matmul_grouped_noalloc": [ctypes.POINTER(StGemm), _i64, _vp],
     "st_f16_enabled": [],
     "st_ndarray_matmul": [_vp, _vp, _vp, _i64, _i64, _i64],
     "st_softmax": [_vp, _vp, _i64, _i64, _i64, _f32, _i32, _i32, _vp],

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(CSRC, "_build")
 LIB = os.path.join(HERE, "libscratchtape_hip.so")
-SOURCES = ["runtime.hip", "gemm.hip", "gemm_dma.hip", "gemm_group.hip", "rows.hip", "knn.hip", "knn_probe.hip", "attn.hip", "peaks.hip"]
+SOURCES = ["runtime.hip", "gemm.hip", "gemm_dma.hip", "gemm_group.hip", "rows.hip", "knn.hip", "knn_probe.hip", "attn.hip", "peaks.hip", "noalloc.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -120,17 +120,19 @@ def matmul_with(a: MatRef, b: MatRef, out: MatRef, batch: int, m: int, k: int, n
     _call("st_matmul_with", a, b, out, batch, m, k, n, epi, int(bool(use_f16)), stream=stream)
 
 
-def matmul_grouped(calls, stream=None) -> None:
+def matmul_grouped(calls, stream=None, noalloc: bool = False) -> None:
     """Several independent `matmul_with` calls in one submission (st_matmul_grouped).
 
     `calls` holds (a, b, out, batch, m, k, n, epi, use_f16) tuples, the arguments
     of matmul_with, e.g. a Linear backward's dW and dx (gpu_step/tape.rs:324-347).
-    No call may read or write memory that another one writes."""
+    No call may read or write memory that another one writes.  noalloc: the
+    same through st_matmul_grouped_noalloc (split-k partials in the library's
+    fixed per-device scratch; no device allocation)."""
     calls = list(calls)
     arr = (_lib.StGemm * max(1, len(calls)))()
     for i, (a, b, out, batch, m, k, n, epi, use_f16) in enumerate(calls):
         arr[i] = _lib.StGemm(a._c(), b._c(), out._c(), (epi or Epilogue())._c(), batch, m, k, n, int(bool(use_f16)), 0)
-    _lib.call("st_matmul_grouped", arr, len(calls), _stream(stream))
+    _lib.call("st_matmul_grouped_noalloc" if noalloc else "st_matmul_grouped", arr, len(calls), _stream(stream))
 
 
 def f16_enabled() -> bool:
