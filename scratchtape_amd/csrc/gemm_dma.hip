@@ -169,13 +169,23 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[i][u], bx8[j][u], acc[i][j], 0, 0, 0);
         }
         if (do_cs && tid < BN) {
-            // This stage's 32 values of column col0 + tid, added in k order.
+            // This stage's 32 values of column col0 + tid in k order: f32 route
+            // one running sum; f16 route, the sum of each 8 consecutive k
+            // (from 0, in order) added in order, as the grouped f16 kernel sums
+            // the columns (each of its lanes holds 8 consecutive k of a column).
             float x[8];
 #pragma unroll
             for (int gg = 0; gg < 4; gg++) {
                 frag<BN, BKC>(lb, tid, gg, x);
+                if constexpr (F16) {
+                    float p = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; e++) cs_acc += x[e];
+                    for (int e = 0; e < 8; e++) p += x[e];
+                    cs_acc += p;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) cs_acc += x[e];
+                }
             }
         }
     };

@@ -437,6 +437,485 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The f16 route: operands staged through registers and converted to f16 once.
+//
+// Eight waves, two per SIMD: four producers and four consumers.  The
+// producers load each k-stage (32 deep) of both f32 operand panels into
+// registers with buffer loads, three stages ahead; one stage before it is
+// multiplied, they round it to f16 (RNE, two values per v_cvt_pk_f16_f32) and
+// write it to the stage's LDS slot as 16-byte runs of 8 consecutive k of one
+// row.  Every element is converted once, and LDS holds f16: the LDS writes
+// and the consumers' fragment reads (one ds_read_b128 per 32 x 32 x 16
+// operand) move half the bytes of an f32 stage.  Operands whose rows are
+// contiguous in memory (A transposed, B not) are transposed in registers: a
+// producer lane loads W consecutive rows on 8 consecutive k-lines and writes
+// W runs of 8 k.  The consumers each own a (TM / 2) x 64 block of the TM x 128
+// tile (v_mfma_f32_32x32x16_f16) and store it straight from the accumulators.
+// A producer and a consumer share each SIMD, so one's loads, conversions and
+// LDS writes overlap the other's matrix-core work.
+//
+// LDS layout of an operand region (rows x 32 k of f16, 64 bytes per row):
+// k-group g (8 k) of row r at p(r) * 64 + 16 (g ^ s(r)), p(r) = r ^ ((r >> 2) &
+// 3), s(r) = (r1 ^ r4) | (r0 ^ r3 ^ r5) << 1 (ri: bit i of r).  The fragment
+// reads (32 consecutive rows x 2 k-groups), the k-contiguous writes (16 rows x
+// 4 groups per wave) and the transposed writes (rows W l + w, one group) each
+// touch every bank once per 16 lanes (64 banks) and per 8 lanes (32 banks).
+//
+// One barrier per stage: stage q is multiplied from slot q % 3 while stage
+// q + 1 is converted into slot (q + 1) % 3 and the loads of stages q + 2 and
+// q + 3 are in flight (three register sets).
+namespace r16 {
+
+constexpr int NSL = 3;  // LDS slots = producer register sets
+
+template <int TM_>
+struct Cfg {
+    static constexpr int TM = TM_, THREADS = 512;
+    static constexpr int WM = TM / 2, WN = 64;         // 2 x 2 consumer waves
+    static constexpr int M32 = WM / 32, N32 = WN / 32;  // 32 x 32 blocks per consumer wave
+    static constexpr int SA = TM * 64, SB = TN * 64;    // bytes of a stage (f16)
+    static constexpr int SLOT = SA + SB;
+    static constexpr int NS = 5;                        // every unit (split slice) keeps NS - 1 = 4 stages
+    static_assert(NSL * SLOT + NSL * 4 * TN * 4 + sizeof(GroupArgs) + 4 * (st::GROUP_MAX + 1) <= 160 * 1024, "LDS");
+};
+using Tall16 = Cfg<256>;
+using Square16 = Cfg<128>;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds_off(int r, int g) {
+    const int p = r ^ ((r >> 2) & 3);
+    const int s = (((r >> 1) ^ (r >> 4)) & 1) | (((r ^ (r >> 3) ^ (r >> 5)) & 1) << 1);
+    return (uint32_t)(p * 64 + 16 * (g ^ s));
+}
+
+// Buffer resource over [p, p + 2^31): offsets are 32-bit from the unit's
+// panel base (checked on the host), no range clamping.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// How one producer lane loads an operand of R rows: 8 loads per stage of
+// R / 64 dwords each.  KC (k contiguous): pair i (= i 256 + lane id) is row
+// i 64 + id / 4, k-group id % 4, 32 bytes in 2 (R = 256) or 4 loads; RC:
+// rows W (id % 64) .. + W - 1 on k-lines 8 (id / 64) + load index.  Load n's
+// source is base + off + st step + (n >> sh) pair + (n & msk) 4 W.
+struct OpRef {
+    const char *base;  // panel base of the unit (its first row / column and k)
+    int32_t step, pair, sh, msk;
+    uint32_t off;  // this lane's byte offset within a stage
+    int32_t kc;
+};
+
+struct Unit16 {
+    int32_t p;  // GEMM index, -1: none
+    int32_t nst, row0, col0, slice, cs;
+    int64_t zb;
+    OpRef a, b;
+};
+
+__device__ __forceinline__ OpRef pick(bool c, const OpRef &x, const OpRef &y) {
+    OpRef o;
+    o.base = c ? x.base : y.base;
+    o.step = c ? x.step : y.step;
+    o.pair = c ? x.pair : y.pair;
+    o.sh = c ? x.sh : y.sh;
+    o.msk = c ? x.msk : y.msk;
+    o.off = c ? x.off : y.off;
+    o.kc = c ? x.kc : y.kc;
+    return o;
+}
+
+template <int R>
+__device__ __forceinline__ void op_ref(OpRef &o, bool kc, const float *base, int64_t ld, int id) {
+    constexpr int W = R / 64;
+    o.kc = kc;
+    o.base = reinterpret_cast<const char *>(base);
+    if (kc) {
+        o.step = 4 * BK;
+        o.pair = (int32_t)(64 * ld * 4);
+        o.sh = W == 4 ? 1 : 2;
+        o.msk = W == 4 ? 1 : 3;
+        o.off = (uint32_t)((id >> 2) * ld * 4 + 32 * (id & 3));
+    } else {
+        o.step = (int32_t)(BK * ld * 4);
+        o.pair = (int32_t)(ld * 4);
+        o.sh = 0;
+        o.msk = 0;
+        o.off = (uint32_t)(8 * (id >> 6) * ld * 4 + 4 * W * (id & 63));
+    }
+}
+
+// The 8 loads of stage st of an operand of R rows.
+template <int R>
+using OpRegs = typename std::conditional<R == 256, u32x4, u32x2>::type;
+
+template <int R>
+__device__ __forceinline__ void load_op(OpRegs<R> (&v)[8], const OpRef &o, int st) {
+    constexpr int W = R / 64;
+    const int32_t s0 = st * o.step;
+    const __amdgpu_buffer_rsrc_t r = rsrc(o.base);
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        // KC: load n is part n & msk (4 W bytes wide) of pair n >> sh; RC:
+        // k-line n (sh = msk = 0).
+        const int32_t so = s0 + (n >> o.sh) * o.pair + (n & o.msk) * (4 * W);
+        if constexpr (R == 256)
+            v[n] = __builtin_amdgcn_raw_buffer_load_b128(r, o.off, so, 0);
+        else
+            v[n] = __builtin_amdgcn_raw_buffer_load_b64(r, o.off, so, 0);
+    }
+}
+
+__device__ __forceinline__ float f_(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ half8 cvt8(float x0, float x1, float x2, float x3, float x4, float x5, float x6,
+                                       float x7) {
+    half8 h;
+    h[0] = (_Float16)x0;
+    h[1] = (_Float16)x1;
+    h[2] = (_Float16)x2;
+    h[3] = (_Float16)x3;
+    h[4] = (_Float16)x4;
+    h[5] = (_Float16)x5;
+    h[6] = (_Float16)x6;
+    h[7] = (_Float16)x7;
+    return h;
+}
+
+// Rounds a loaded stage of an operand of R rows to f16 and writes it to its
+// LDS region.
+template <int R>
+__device__ __forceinline__ void store_op(const OpRegs<R> (&v)[8], bool kc, char *region, int id) {
+    constexpr int W = R / 64;
+    if (kc) {
+        const uint32_t a = lds_off(id >> 2, id & 3);
+#pragma unroll
+        for (int i = 0; i < R / 64; i++) {
+            half8 h;
+            if constexpr (W == 4)
+                h = cvt8(f_(v[2 * i][0]), f_(v[2 * i][1]), f_(v[2 * i][2]), f_(v[2 * i][3]), f_(v[2 * i + 1][0]),
+                         f_(v[2 * i + 1][1]), f_(v[2 * i + 1][2]), f_(v[2 * i + 1][3]));
+            else
+                h = cvt8(f_(v[4 * i][0]), f_(v[4 * i][1]), f_(v[4 * i + 1][0]), f_(v[4 * i + 1][1]),
+                         f_(v[4 * i + 2][0]), f_(v[4 * i + 2][1]), f_(v[4 * i + 3][0]), f_(v[4 * i + 3][1]));
+            *reinterpret_cast<half8 *>(region + a + i * 4096) = h;
+        }
+    } else {
+        const int rg = id & 63, g = id >> 6;
+#pragma unroll
+        for (int w = 0; w < W; w++)
+            *reinterpret_cast<half8 *>(region + lds_off(W * rg + w, g)) =
+                cvt8(f_(v[0][w]), f_(v[1][w]), f_(v[2][w]), f_(v[3][w]), f_(v[4][w]), f_(v[5][w]), f_(v[6][w]),
+                     f_(v[7][w]));
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void locate16(const GroupArgs &ga, const int32_t *cum, int x, int j, int lane, int id, Unit16 &u) {
+    const int count = ga.count;
+    const bool before = lane < count && cum[lane + 1] <= j;
+    const int p = __popcll(__ballot(before));
+    u.p = p < count ? p : -1;
+    if (u.p < 0) return;
+    const GProb &g = ga.p[p];
+    const int tiles_n = uni(g.tiles_n), tiles_m = uni(g.tiles_m), splits = uni(g.splits), slice_k = uni(g.slice_k);
+    const int flags = uni(g.flags), lda = uni(g.lda), ldb = uni(g.ldb);
+    const int t = block_start(x, uni(g.units)) + j - uni(cum[p]);
+    const int bx = t % tiles_n;
+    const int r = t / tiles_n;
+    const int by = r % tiles_m;
+    const int zs = r / tiles_m;
+    u.zb = zs / splits;
+    u.slice = zs % splits;
+    u.row0 = by * C::TM;
+    u.col0 = bx * TN;
+    const int kbeg = u.slice * slice_k;
+    u.nst = (min(uni(g.k), kbeg + slice_k) - kbeg) / BK;
+    u.cs = (flags & F_CS) && u.row0 == 0;
+    const bool akc = !(flags & F_TA), bkc = (flags & F_TB) != 0;
+    const float *a = uni(g.a + zoff(u.zb, g.a_group, g.a_stride, g.a_inner) +
+                         (akc ? (int64_t)u.row0 * lda + kbeg : (int64_t)kbeg * lda + u.row0));
+    const float *b = uni(g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner) +
+                         (bkc ? (int64_t)u.col0 * ldb + kbeg : (int64_t)kbeg * ldb + u.col0));
+    op_ref<C::TM>(u.a, akc, a, lda, id);
+    op_ref<TN>(u.b, bkc, b, ldb, id);
+}
+
+// grid: a multiple of 8 workgroups, at most one per CU.  Every unit has at
+// least 4 k-stages (so the loads, at most 3 stages ahead, never reach past
+// the next unit).
+template <class C>
+__global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
+    constexpr int TM = C::TM, SA = C::SA, SLOT = C::SLOT;
+    constexpr int WM = C::WM, M32 = C::M32, N32 = C::N32;
+    __shared__ __attribute__((aligned(16))) char lds[NSL * SLOT];
+    __shared__ float csp[NSL][4][TN];  // column-sum partials of B per stage slot and k-group
+    __shared__ GroupArgs sga;
+    __shared__ int32_t cum[st::GROUP_MAX + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool producer = __builtin_amdgcn_readfirstlane(wave) >= 4;
+    const int id = tid & 255;  // lane id within the producers (or the consumers)
+    const int wm = (wave >> 1) & 1, wn = wave & 1;
+    const int x = blockIdx.x % XCDS, L = gridDim.x / XCDS;
+    const int w = blockIdx.x / XCDS;
+    load_args(ga, sga, cum, x, tid, C::THREADS);
+
+    const int nlist = uni(cum[sga.count]), sched = uni(sga.sched);
+    auto next_pos = [&](int prev) __attribute__((always_inline)) -> int {
+        if (!sched) return min(prev < 0 ? w : prev + L, nlist);
+        for (int base = prev + 1; base < nlist; base += 64) {
+            const int i = base + lane;
+            const uint64_t mine = __ballot(i < nlist && sga.owner[x][i] == w);
+            if (mine) return base + __builtin_ctzll(mine);
+        }
+        return nlist;
+    };
+    int j = next_pos(-1), jn = next_pos(j);
+    Unit16 cur, nxt;
+    locate16<C>(sga, cum, x, j, lane, id, cur);
+    if (cur.p < 0) return;
+    locate16<C>(sga, cum, x, jn, lane, id, nxt);
+
+    int st = 0;  // stage of cur being multiplied
+
+    // ---- producer state: NSL register sets --------------------------------
+    OpRegs<TM> va[NSL][8];
+    OpRegs<TN> vb[NSL][8];
+    // The load cursor: the unit the next loads come from (its operand
+    // references by value, lu = 0 cur, 1 nxt) and its stage.  Kept apart from
+    // cur / nxt so that the lane offsets the loads use change only when the
+    // cursor enters a new unit.
+    OpRef la = cur.a, lb = cur.b;
+    int lst = 0, lnst = cur.nst, lu = 0;
+    bool lvalid = true;
+    // Loads the cursor's stage into register set S.  Past the workgroup's
+    // last stage the loads still go out (re-reading the last unit's first
+    // stage, never multiplied), so that every step has the same 16 loads in
+    // flight and the compiler's waits before each conversion count the two
+    // younger stages' loads exactly.
+    auto issue = [&](auto set_c) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value;
+        load_op<TM>(va[S], la, lvalid ? lst : 0);
+        load_op<TN>(vb[S], lb, lvalid ? lst : 0);
+        if (lvalid && ++lst == lnst) {
+            // The loads run at most 3 stages ahead of the multiplication and
+            // every unit has 4 or more: only cur's loads can run out here.
+            if (lu == 0 && nxt.p >= 0) {
+                la = nxt.a;
+                lb = nxt.b;
+                lst = 0;
+                lnst = nxt.nst;
+                lu = 1;
+            } else {
+                lvalid = false;
+            }
+        }
+    };
+    auto convert = [&](auto set_c, int ahead) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value;
+        const int s = st + ahead;
+        const bool in_cur = s < cur.nst, none = !in_cur && nxt.p < 0;
+        // Past the last stage the dummy loads are converted too, into a slot
+        // nobody reads again: every register set is waited for on every path.
+        const bool akc = in_cur || none ? cur.a.kc : nxt.a.kc, bkc = in_cur || none ? cur.b.kc : nxt.b.kc;
+        const bool cs = !none && (in_cur ? cur.cs : nxt.cs);
+        store_op<TM>(va[S], akc, lds + S * SLOT, id);
+        store_op<TN>(vb[S], bkc, lds + S * SLOT + SA, id);
+        if (cs) {
+            // B is row-contiguous here (the f16 route sums columns only then):
+            // this lane holds columns 2 (id % 64) + w2 on k 8 (id / 64) .. + 7.
+#pragma unroll
+            for (int w2 = 0; w2 < 2; w2++) {
+                float p = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) p += f_(vb[S][jj][w2]);
+                csp[S][id >> 6][2 * (id & 63) + w2] = p;
+            }
+        }
+    };
+
+    // ---- consumer state ---------------------------------------------------
+    // Fragment read addresses (fixed for the kernel): lane l reads row l % 32
+    // of its 32-row block, k-group 2 ks + l / 32.
+    uint32_t ra[M32][2], rb[N32][2];
+#pragma unroll
+    for (int i = 0; i < M32; i++)
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) ra[i][ks] = lds_off(wm * WM + i * 32 + (lane & 31), 2 * ks + (lane >> 5));
+#pragma unroll
+    for (int i = 0; i < N32; i++)
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) rb[i][ks] = SA + lds_off(wn * 64 + i * 32 + (lane & 31), 2 * ks + (lane >> 5));
+    f32x16 acc[M32][N32];
+#pragma unroll
+    for (int i = 0; i < M32; i++)
+#pragma unroll
+        for (int n = 0; n < N32; n++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][n][e] = 0.f;
+    float cs_acc = 0.f;  // column col0 + id of B summed over this unit's k (consumers, id < 128)
+
+    auto lds_fence_bar = [&]() __attribute__((always_inline)) {
+        // this wave's LDS writes done (vector-memory loads stay in flight),
+        // then the workgroup barrier
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        bar();
+    };
+
+    // The epilogue of cur, straight from the accumulators: lane l holds
+    // column l % 32 of each 32 x 32 block and rows 8 (e / 4) + 4 (l / 32) +
+    // e % 4 of it.
+    auto epilogue = [&]() __attribute__((always_inline)) {
+        const GProb &g = sga.p[cur.p];
+        const int gflags = uni(g.flags), gsplits = uni(g.splits);
+        const bool split = gsplits > 1;
+        float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
+        const int64_t o0 = uni(split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner));
+        const int64_t ld = uni((int64_t)(split ? g.n : g.ldo));
+        float *const obase = uni(split ? P : g.out + o0);
+        const float *const bias = uni(g.bias), *const mask = uni(g.mask), *const res = uni(g.res);
+        const int64_t lane_off = (int64_t)(4 * (lane >> 5)) * ld + (lane & 31);
+#pragma unroll
+        for (int n = 0; n < N32; n++) {
+            const int c0 = cur.col0 + wn * 64 + n * 32;
+            float bv = 0.f;
+            if (!split && bias) bv = bias[cur.zb * g.bias_stride + c0 + (lane & 31)];
+#pragma unroll
+            for (int i = 0; i < M32; i++) {
+                const int64_t r0 = cur.row0 + wm * WM + i * 32;
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) v[e] = acc[i][n][e];
+                auto idx = [&](int e) __attribute__((always_inline)) { return (r0 + 8 * (e >> 2) + (e & 3)) * ld + c0 + lane_off; };
+                if (!split) {
+                    if (bias) {
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] += bv;
+                    }
+                    if (gflags & F_RELU) {
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] = v[e] < 0.f ? 0.f : v[e];
+                    }
+                    if (mask) {
+                        float t[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) t[e] = mask[o0 + idx(e)];
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            if (t[e] <= 0.f) v[e] = 0.f;
+                    }
+                    if (res) {
+                        float t[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) t[e] = res[o0 + idx(e)];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] += t[e];
+                    }
+                    if (gflags & F_ACC) {
+                        float t[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) t[e] = obase[idx(e)];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] += t[e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) obase[idx(e)] = v[e];
+            }
+        }
+        if (cur.cs && id < TN) {
+            if (split)
+                g.cs[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + id] = cs_acc;
+            else
+                g.cs[cur.zb * g.cs_stride + cur.col0 + id] += cs_acc;
+        }
+    };
+
+    // Moves to the next unit once cur's last stage is done; false when the
+    // workgroup has none left.
+    auto advance = [&]() __attribute__((always_inline)) -> bool {
+        if (nxt.p < 0) return false;
+        cur = nxt;
+        st = 0;
+        lu = 0;  // the load cursor was in nxt
+        j = jn;
+        jn = next_pos(j);
+        locate16<C>(sga, cum, x, jn, lane, id, nxt);
+        return true;
+    };
+
+    // The two roles run separate loops (so their registers never live at the
+    // same time) with the same barriers: one per stage, plus the prologue's.
+    if (producer) {
+        // Prologue: stages 0, 1, 2 of cur in flight; stage 0 into slot 0.
+        issue(std::integral_constant<int, 0>());
+        issue(std::integral_constant<int, 1>());
+        issue(std::integral_constant<int, 2>());
+        convert(std::integral_constant<int, 0>(), 0);
+        lds_fence_bar();
+        // Stage q (slot S): load stage q + 3 into register set S, convert
+        // stage q + 1 into slot S + 1.
+        auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
+            constexpr int S = decltype(set_c)::value;
+            // Stages q + 1 and q + 2 (16 loads each) are in flight, stage q's
+            // loads are done: a no-op wait that tells the compiler so, which it
+            // cannot work out through the loop's back edge by itself.
+            wait_vm<32>();
+            issue(set_c);
+            convert(std::integral_constant<int, (S + 1) % NSL>(), 1);
+            lds_fence_bar();
+            return ++st < cur.nst || advance();
+        };
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>()) &&
+               step(std::integral_constant<int, 2>())) {
+        }
+    } else {
+        lds_fence_bar();
+        // Stage q: multiply slot S.
+        auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
+            constexpr int S = decltype(set_c)::value;
+            const char *slot = lds + S * SLOT;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                half8 af[M32], bf[N32];
+#pragma unroll
+                for (int i = 0; i < M32; i++) af[i] = *reinterpret_cast<const half8 *>(slot + ra[i][ks]);
+#pragma unroll
+                for (int n = 0; n < N32; n++) bf[n] = *reinterpret_cast<const half8 *>(slot + rb[n][ks]);
+#pragma unroll
+                for (int i = 0; i < M32; i++)
+#pragma unroll
+                    for (int n = 0; n < N32; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[n], acc[i][n], 0, 0, 0);
+            }
+            if (cur.cs && id < TN) {
+#pragma unroll
+                for (int g = 0; g < 4; g++) cs_acc += csp[S][g][id];
+            }
+            lds_fence_bar();
+            if (++st < cur.nst) return true;
+            epilogue();
+#pragma unroll
+            for (int i = 0; i < M32; i++)
+#pragma unroll
+                for (int n = 0; n < N32; n++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][n][e] = 0.f;
+            cs_acc = 0.f;
+            return advance();
+        };
+        while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>()) &&
+               step(std::integral_constant<int, 2>())) {
+        }
+    }
+}
+
+}  // namespace r16
+
 struct SProb {
     const float *part;
     float *out;
@@ -521,6 +1000,12 @@ bool group_eligible(const DmaGemm &d) {
     if (!fits32(d.lda) || !fits32(d.ldb) || !fits32(d.ldo) || !fits32(d.a_group) || !fits32(d.b_group) ||
         !fits32(d.o_group))
         return false;
+    // The f16 kernel addresses a unit's operand panels with 32-bit buffer
+    // offsets below 2^31: up to 256 rows and all of k past the panel base.
+    if (d.f16) {
+        const auto panel_ok = [&](int64_t ld) { return (d.k + 256) * ld * 4 + 4096 < ((int64_t)1 << 31); };
+        if (!panel_ok(d.lda) || !panel_ok(d.ldb)) return false;
+    }
     return fits32(d.batch * (d.m / Square::TM) * (d.n / TN) * (d.k / BK));
 }
 
@@ -590,7 +1075,7 @@ void schedule(GroupArgs &ga, int L) {
 }
 
 template <class C>
-st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_t stream) {
+st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupArgs), hipStream_t stream) {
     using st::DmaGemm;
     using st::fail;
     constexpr int TM = C::TM, NS = C::NS;
@@ -716,7 +1201,6 @@ st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_
     }
     const int64_t wgs = std::min<int64_t>(cus / XCDS * XCDS, cdiv(units, XCDS) * XCDS);
     schedule(ga, (int)std::max<int64_t>(1, wgs / XCDS));
-    void (*kern)(GroupArgs) = f16 ? &k_gemm_group<C, true> : &k_gemm_group<C, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)std::max<int64_t>(XCDS, wgs)), dim3(C::THREADS), 0, stream, ga);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && sa.count) {
@@ -731,7 +1215,11 @@ st_status launch_group(const st::DmaGemm *items, int count, bool f16, hipStream_
 namespace st {
 
 st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream) {
-    return tall ? launch_group<Tall>(items, count, f16, stream) : launch_group<Square>(items, count, f16, stream);
+    if (f16)
+        return tall ? launch_group<r16::Tall16>(items, count, &r16::k_gemm_group16<r16::Tall16>, stream)
+                    : launch_group<r16::Square16>(items, count, &r16::k_gemm_group16<r16::Square16>, stream);
+    return tall ? launch_group<Tall>(items, count, &k_gemm_group<Tall, false>, stream)
+                : launch_group<Square>(items, count, &k_gemm_group<Square, false>, stream);
 }
 
 }  // namespace st
