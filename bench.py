@@ -771,12 +771,12 @@ def main():
             sys.exit(3)
         graph16 = t16["grouped"]["graph_ms"]
         value = ss16.flops / graph16 / 1e9
-        # The dominant kernel is the grouped launch itself (k_gemm_group, plus the split-k sum k_sum_group):
+        # The dominant kernel is the grouped launch itself (k_gemm_group16, plus the split-k sum k_sum_group):
         # the set's flops and algorithmic bytes over its time per step with the K timed steps replayed as one
         # HIP graph, from HIP events on its stream.
-        roof = roofline("k_gemm_group f16 (+ k_sum_group): the 15-GEMM set in one grouped call", ss16.flops,
+        roof = roofline("k_gemm_group16 (+ k_sum_group): the 15-GEMM f16 set in one grouped call", ss16.flops,
                         ss16.bytes, graph16,
-                        traffic_for("k_gemm_group f16 step set", "scratchtape_amd/csrc/gemm_group.hip"))
+                        traffic_for("k_gemm_group16 f16 step set", "scratchtape_amd/csrc/gemm_group.hip"))
         extra["c3_f16_set"] = dict(flops=ss16.flops, algorithmic_bytes=ss16.bytes,
                                    per_gemm_bytes=ss16.per_gemm_bytes, graph_ms=graph16,
                                    tflops=round(value, 2), mfma_frac=round(value / PEAK["f16"], 4),

@@ -24,7 +24,7 @@ def test_traffic_is_quoted_only_for_the_profiled_source():
     with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
         table = json.load(f)
     for key, e in table.items():
-        src = {"k_gemm_group f16 step set": "scratchtape_amd/csrc/gemm_group.hip",
+        src = {"k_gemm_group16 f16 step set": "scratchtape_amd/csrc/gemm_group.hip",
                "k_search": "scratchtape_amd/csrc/knn.hip", "k_search masked": "scratchtape_amd/csrc/knn.hip",
                "st_knn_probe": "scratchtape_amd/csrc/knn_probe.hip", "k_attn fused step": "scratchtape_amd/csrc/attn.hip",
                "k_ln step": "scratchtape_amd/csrc/rows.hip"}[key]
