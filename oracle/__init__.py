@@ -115,6 +115,8 @@ def lib():
         L.orc_knn_search_masked.argtypes = [_u8p, _f32p, _i64, _f32p, _i64p, _i64p, _i64, _i64, _i64, _i64, _i64p,
                                              _f32p]
         L.orc_knn_ref_f16_dist.argtypes = [_u8p, ctypes.c_float, ctypes.c_float, _f32p, _i64]
+        L.orc_knn_ref_f16_dists.argtypes = [_u8p, _f32p, _f32p, _i64, _i64, _i64, _f32p, _f32p]
+        L.orc_knn_ref_f16_probe.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _i64, _i32p]
         L.orc_layer_norm.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_float, _i64, _i64, _f32p, _f32p, _f32p]
         L.orc_layer_norm_backward.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p, _f32p, _i64, _f32p, _i32,
                                               _i64, _i64]
@@ -348,6 +350,27 @@ def knn_search_masked(codes, scales, queries, lo, hi, always=0, k=128):
 def knn_ref_f16_dist(code_row, scale, norm_f16, q):
     return lib().orc_knn_ref_f16_dist(np.ascontiguousarray(code_row, np.uint8), float(scale), float(norm_f16),
                                       np.ascontiguousarray(q, np.float32), q.size)
+
+
+def knn_ref_f16_dists(codes, scales, norm_f16, r0, r1, q):
+    """knn_ref_f16_dist for keys r0..r1 of a store against one query: float32 [r1 - r0]."""
+    codes = np.ascontiguousarray(codes, np.uint8).reshape(-1)
+    scales = np.ascontiguousarray(scales, np.float32)
+    d = (codes.size // scales.size) * 4
+    out = np.empty(r1 - r0, np.float32)
+    lib().orc_knn_ref_f16_dists(codes, scales, np.ascontiguousarray(norm_f16, np.float32), d, r0, r1,
+                                np.ascontiguousarray(q, np.float32), out)
+    return out
+
+
+def knn_ref_f16_probe(cent: np.ndarray, queries: np.ndarray, nprobe: int) -> np.ndarray:
+    """The reference's f16 probe ranking (ivf.rs:62-67, 470-485, 131-161): int32 [nq, nprobe], nearest first."""
+    cent = np.ascontiguousarray(cent, np.float32)
+    queries = np.ascontiguousarray(queries, np.float32)
+    nq, d = queries.shape
+    out = np.empty((nq, nprobe), np.int32)
+    lib().orc_knn_ref_f16_probe(cent.reshape(-1), cent.shape[0], queries.reshape(-1), nq, d, nprobe, out.reshape(-1))
+    return out
 
 
 def knn_centroid_prep(cent: np.ndarray):

@@ -656,6 +656,83 @@ float orc_knn_ref_f16_dist(const uint8_t *code, float s, float norm_f16, const f
     return qn + norm_f16 - 2.0f * dot;
 }
 
+/* orc_knn_ref_f16_dist for every key of rows [r0, r1) against one query, into
+ * out[r - r0] (same arithmetic; the four f16 key values of a key are rounded
+ * once).  Fidelity measurement only: the reference's ranking next to the
+ * exact integer contract's. */
+void orc_knn_ref_f16_dists(const uint8_t *codes, const float *scales, const float *norm_f16, int64_t d,
+                           int64_t r0, int64_t r1, const float *q, float *out) {
+    float *qv = (float *)malloc(sizeof(float) * (size_t)d);
+    float qn = 0.0f;
+    for (int64_t i = 0; i < d; i++) {
+        qv[i] = orc_round_f16(q[i]);
+        qn += qv[i] * qv[i];
+    }
+    const int64_t kb = d / 4;
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t r = r0; r < r1; r++) {
+        const uint8_t *code = codes + r * kb;
+        float lut[4];
+        for (int u = 0; u < 4; u++) lut[u] = orc_round_f16(((float)u - 1.5f) * scales[r]);
+        float dot = 0.0f;
+        for (int64_t i = 0; i < d; i++) dot += qv[i] * lut[(code[i >> 2] >> (2 * (i & 3))) & 3];
+        out[r - r0] = qn + norm_f16[r] - 2.0f * dot;
+    }
+    free(qv);
+}
+
+/* The reference's probe ranking (ivf.rs:62-67 `Cent::new`, ivf.rs:470-485 and
+ * `k_probe` ivf.rs:131-161), for fidelity measurement: centroids and queries
+ * rounded to f16, cnorm[c] = sum of the f16 centroid's squares in f32, dot =
+ * the f16 products summed in f32 (index order here; the reference's matrix
+ * cores may sum in another order), dd = cnorm - 2 dot, and the nprobe
+ * smallest by insertion with strict <, so equal dd keep the lower cell. */
+void orc_knn_ref_f16_probe(const float *cent, int64_t nlist, const float *queries, int64_t nq, int64_t d,
+                           int64_t nprobe, int32_t *probes) {
+    float *c16 = (float *)malloc(sizeof(float) * (size_t)(nlist * d));
+    float *cnorm = (float *)malloc(sizeof(float) * (size_t)nlist);
+    for (int64_t c = 0; c < nlist; c++) {
+        float s = 0.0f;
+        for (int64_t i = 0; i < d; i++) {
+            const float x = orc_round_f16(cent[c * d + i]);
+            c16[c * d + i] = x;
+            s += x * x;
+        }
+        cnorm[c] = s;
+    }
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t qi = 0; qi < nq; qi++) {
+        float *qv = (float *)malloc(sizeof(float) * (size_t)d);
+        float *bd = (float *)malloc(sizeof(float) * (size_t)nprobe);
+        int32_t *bi = (int32_t *)malloc(sizeof(int32_t) * (size_t)nprobe);
+        for (int64_t i = 0; i < d; i++) qv[i] = orc_round_f16(queries[qi * d + i]);
+        for (int64_t j = 0; j < nprobe; j++) {
+            bd[j] = 3.0e38f;
+            bi[j] = 0;
+        }
+        for (int64_t c = 0; c < nlist; c++) {
+            float dot = 0.0f;
+            for (int64_t i = 0; i < d; i++) dot += qv[i] * c16[c * d + i];
+            const float dd = cnorm[c] - 2.0f * dot;
+            if (!(dd < bd[nprobe - 1])) continue;
+            int64_t pos = nprobe - 1;
+            while (pos > 0 && bd[pos - 1] > dd) {
+                bd[pos] = bd[pos - 1];
+                bi[pos] = bi[pos - 1];
+                pos--;
+            }
+            bd[pos] = dd;
+            bi[pos] = (int32_t)c;
+        }
+        for (int64_t j = 0; j < nprobe; j++) probes[qi * nprobe + j] = bi[j];
+        free(bi);
+        free(bd);
+        free(qv);
+    }
+    free(cnorm);
+    free(c16);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Probe selection: each query's nprobe nearest IVF cells.                   */
 /* ------------------------------------------------------------------------ */
