@@ -69,3 +69,26 @@ def test_layer_norm_at_the_step_shape(dev):
 
 def test_layer_norm_two_models_with_strided_parameter_sets(dev):
     run_case(dev, 2 * 300, 100, 4, models=2, stride=3 * 100 + 7, seed=13)
+
+
+# The vector forms (d % 4 == 0 up to 1024, 16-byte aligned rows and parameter sets): the backward's row pass
+# writes dx and per-16-row-chunk column partials, a second launch adds the chunks (one or several per slice).
+@pytest.mark.parametrize("nrows,d,off", [(37, 24, 4), (203, 200, 8), (600, 520, 0), (300, 1024, 4), (5, 256, 0)])
+def test_layer_norm_vector_forms(dev, nrows, d, off):
+    run_case(dev, nrows, d, off, seed=nrows + d)
+
+
+def test_layer_norm_vector_forms_three_models(dev):
+    # 272 rows per model: 17 chunks per model, over sixteen slices of two chunks (the last slice empty).
+    run_case(dev, 3 * 272, 64, 8, models=3, stride=2 * 64 + 12, seed=17)
+
+
+@pytest.mark.parametrize("nrows,d,off", [(64, 1028, 0), (64, 250, 0), (64, 256, 2)])
+def test_layer_norm_falls_back_off_the_vector_forms(dev, nrows, d, off):
+    run_case(dev, nrows, d, off, seed=3)
+
+
+def test_layer_norm_back_to_back_shapes(dev):
+    """Calls of different shapes back to back, each checked (the row scratch arena is reused across them)."""
+    for nrows, d in [(4096, 256), (37, 24), (600, 520), (4096, 256)]:
+        run_case(dev, nrows, d, 0, seed=nrows)
