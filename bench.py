@@ -642,12 +642,12 @@ class ProbeBench:
         self.c = knn.Centroids(self.cent)
         self.queries = queries
         self.out = torch.empty((self.NQ, self.NPROBE), dtype=torch.int32, device=dev)
-        ncb, nqb = -(-self.NLIST // 8), -(-self.NQ // 8)
+        nct, nqt = -(-self.NLIST // 16), -(-self.NQ // 16)
         # Algorithmic bytes: the centroid store (512 B of digits + 12 B of exponent and norm per cell), the f32
-        # queries and the probe ids.  Matrix-core work: 4 k-steps of one 16x16x64 i8 MFMA per (query block,
-        # centroid block), i.e. the four digit products of every query-centroid dot.
+        # queries and the probe ids.  Matrix-core work: 8 k-steps of one 32x32x32 i8 MFMA per (query tile,
+        # centroid tile) of 16 vectors each, i.e. the four digit products of every query-centroid dot.
         self.bytes = self.NLIST * (512 + 12) + self.NQ * self.D * 4 + self.NQ * self.NPROBE * 4
-        self.ops = nqb * ncb * 4 * 2 * 16 * 16 * 64
+        self.ops = nqt * nct * 8 * 2 * 32 * 32 * 32
 
     def probe(self, i):
         return self.c.probe(self.queries[i % len(self.queries)], self.NPROBE, out=self.out)
@@ -844,7 +844,7 @@ def main():
             sys.exit(3)
         pms, ptiming = pb.run(stream, args.steps, args.warmup)
         probe = dict(ms_per_batch=round(pms, 5), **ptiming, queries_per_s=round(pb.NQ / pms * 1e3, 1),
-                     roofline=roofline("st_knn_probe (k_probe_prep + k_probe_dots + k_probe_select)", pb.ops,
+                     roofline=roofline("st_knn_probe (k_probe_prep + k_probe_part + k_probe_merge)", pb.ops,
                                        pb.bytes, pms,
                                        traffic_for("st_knn_probe", "scratchtape_amd/csrc/knn_probe.hip"), route="i8"))
         if not args.no_cpu:

@@ -14,34 +14,55 @@
 // with cnorm = ldexp(sum C_i^2, 2 ce) (exact), and the cells are ranked by
 // (dd, cell id).  The CPU oracle restates the same arithmetic.
 //
-// Design.  The int16 values are split into two int8 digits, X = 256 Xh + Xl
-// with Xl in [-128, 127] and Xh in [-64, 64], so one i8 MFMA
-// (16 x 16 x 64, int32 accumulate) yields all four digit products of 8
-// queries x 8 centroids over 64 dims: A rows are (query, digit), B columns
-// (centroid, digit), and dot = 65536 hh + 256 (hl + lh) + ll is assembled
-// from two neighbouring lanes.  Digits are stored "MFMA-native": a block of
-// 8 vectors is 4 KiB, [k-step s][lane][16 bytes], so each operand load is one
-// fully coalesced 1 KiB read.  Three kernels:
-//   k_probe_prep   vectors -> digit blocks, exponent (and norm for centroids);
-//   k_probe_dots   dd for a chunk of queries x every centroid (float64, in the
-//                  library's scratch arena);
-//   k_probe_select one workgroup per query: a threshold from the per-thread
-//                  minima keeps about nprobe candidates per round of cells,
-//                  which one wave sorts by (dd, id).
+// Digits.  The int16 values are split into two int8 digits, X = 256 Xh + Xl
+// with Xl in [-128, 127] and Xh in [-64, 64].  One v_mfma_i32_32x32x32_i8
+// takes A rows = 16 queries x {high, low} and B columns = 16 centroids x
+// {high, low} over 32 dims, so its 32 x 32 int32 outputs are all four digit
+// products of 256 query-centroid pairs, and dot = 65536 hh + 256 (hl + lh) +
+// ll is assembled from two neighbouring lanes.  Both operands use one
+// "MFMA-native" tile layout of 16 vectors (8 KiB): [k-step s][lane][16 bytes],
+// lane l holding vector (l % 32) / 2, digit l % 2, dims 32 s + 16 (l / 32) ..
+// + 15, so an operand is one ds_read_b128 per k-step.
+//
+// Three launches per chunk of queries:
+//   k_probe_prep  the queries into digit tiles (as the centroids are, once per
+//                 index) and exponents;
+//   k_probe_part  grid = centroid slices (up to 12 tiles) x groups of 64
+//                 queries.  The workgroup stages its slice in LDS and each wave
+//                 scores its 16 queries against it, keeping the 12 x 4
+//                 order-preserving dd keys of its lane in registers.  A
+//                 per-query threshold -- the nprobe-th smallest of the 16
+//                 per-lane minima, so at least nprobe keys lie at or below it
+//                 and with them the slice's top nprobe -- leaves a few
+//                 candidates per (query, slice), which go to a fixed slot of
+//                 the scratch arena.  A slot that would overflow gets the
+//                 slice's exact top nprobe instead (successive minima over the
+//                 registers).
+//   k_probe_merge one wave per query: the exact top nprobe by (dd, id) over
+//                 its slots' candidates.
+// A k_probe_part workgroup is 8 waves: two per query tile, each scoring half
+// of the slice's tiles (two waves per SIMD hide each other's latencies).
+// dd never leaves the chip; per query only the candidates (about nprobe per
+// slice) are written and read back.
 #include "common.h"
 
 #pragma clang fp contract(off)
 
 namespace {
 
-constexpr int D = 256;              // vector width (the scan's key width)
-constexpr int BLK = 8;              // vectors per digit block
-constexpr int BLK_BYTES = BLK * 2 * D;  // 4096
-constexpr int PROBE_MAX = 16;       // ivf.rs:126
-constexpr int PER_MAX = 8;          // centroid blocks per dots workgroup (staged in LDS)
-constexpr int64_t DD_BUDGET = 256ll << 20;  // bytes of dd per query chunk
+constexpr int D = 256;                     // vector width (the scan's key width)
+constexpr int TILE = 16;                   // vectors per digit tile
+constexpr int TILE_BYTES = TILE * 2 * D;   // 8192
+constexpr int PROBE_MAX = 16;              // ivf.rs:126
+constexpr int QG = 64;                     // queries per k_probe_part workgroup (4 query tiles x 16)
+constexpr int TPS = 12;                    // centroid tiles per slice, at most
+constexpr int HT = TPS / 2;                // tiles per wave (two waves per query tile)
+constexpr int PART_T = 512;                // k_probe_part threads
+constexpr int CAPQ = 64;                   // candidate slot per (query, slice)
+constexpr int64_t CAND_BUDGET = 256ll << 20;  // bytes of candidate slots per query chunk
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -49,17 +70,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// One wave per vector (row r of x [n, D]); lane L handles dims 4L .. 4L + 3.
-// Writes the vector's two digit planes into its block (rows n .. of the last
-// block are zero), its exponent, and, when norm != nullptr, its squared norm.
-// Byte (s, lane, j) of a block is dim 64 s + 16 (lane / 16) + j of vector
-// (lane % 16) / 2, digit lane % 2 (0: high, 1: low).
+// The quantisation of one vector value: X = clamp(rint(v / 2^(e - 14))) and
+// its two digits.  ldexpf is exact here (|result| < 2^14).
+__device__ __forceinline__ void digits_of(float v, int e, int32_t &xh, int32_t &xl, int32_t &X) {
+    X = (int32_t)fminf(fmaxf(rintf(ldexpf(v, 14 - e)), -16384.f), 16383.f);
+    xl = ((X + 128) & 255) - 128;
+    xh = (X - xl) >> 8;
+}
+
+// One wave per vector r (rows n .. of the last tile are zero); lane L
+// handles dims 4L .. 4L + 3, which sit in k-step L / 8, lane half (L % 8) / 4,
+// bytes 4 (L % 4) ..: the two digit words go to lanes 32 h + 2 v (high) and
+// + 1 (low) of the tile, v = r % 16.  Also writes the exponent and, when norm
+// is not null (centroids), the exact squared norm.
 __global__ __launch_bounds__(256) void k_probe_prep(const float *__restrict__ x, int64_t n, int8_t *__restrict__ dig,
                                                     int32_t *__restrict__ ex, double *__restrict__ norm) {
     const int lane = threadIdx.x & 63;
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t nblk = (n + BLK - 1) / BLK;
-    if (r >= nblk * BLK) return;
+    const int64_t ntile = (n + TILE - 1) / TILE;
+    if (r >= ntile * TILE) return;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (r < n) {
         const float4 f = reinterpret_cast<const float4 *>(x + r * D)[lane];
@@ -75,19 +104,17 @@ __global__ __launch_bounds__(256) void k_probe_prep(const float *__restrict__ x,
     int32_t s2 = 0;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        // ldexpf is exact here (|result| < 2^14), and equals x / 2^(e-14).
-        const int32_t X = (int32_t)fminf(fmaxf(rintf(ldexpf(v[t], 14 - e)), -16384.f), 16383.f);
-        const int32_t xl = ((X + 128) & 255) - 128;
-        const int32_t xh = (X - xl) >> 8;
+        int32_t xh, xl, X;
+        digits_of(v[t], e, xh, xl, X);
         lo |= (uint32_t)(xl & 255) << (8 * t);
         hi |= (uint32_t)(xh & 255) << (8 * t);
         s2 += X * X;
     }
-    const int v8 = (int)(r % BLK);
-    const int s = lane >> 4, g = (lane & 15) >> 2, j0 = 4 * (lane & 3);
-    int8_t *blk = dig + (r / BLK) * BLK_BYTES + s * 1024 + j0;
-    *reinterpret_cast<uint32_t *>(blk + (16 * g + 2 * v8) * 16) = hi;
-    *reinterpret_cast<uint32_t *>(blk + (16 * g + 2 * v8 + 1) * 16) = lo;
+    const int vt = (int)(r % TILE);
+    const int s = lane >> 3, h = (lane & 7) >> 2, b0 = 4 * (lane & 3);
+    int8_t *blk = dig + (r / TILE) * TILE_BYTES + s * 1024 + b0;
+    *reinterpret_cast<uint32_t *>(blk + (32 * h + 2 * vt) * 16) = hi;
+    *reinterpret_cast<uint32_t *>(blk + (32 * h + 2 * vt + 1) * 16) = lo;
     if (r >= n) return;
     if (norm) {
         double t2 = (double)s2;  // partial sums are integers below 2^53: exact in any order
@@ -96,98 +123,6 @@ __global__ __launch_bounds__(256) void k_probe_prep(const float *__restrict__ x,
         if (lane == 0) norm[r] = ldexp(t2, 2 * (e - 14));
     }
     if (lane == 0) ex[r] = e - 14;
-}
-
-// dd[q][c] for queries [q0, q0 + nqc) of the chunk (digit blocks qdig, exponents
-// qex, chunk-relative) against centroids [0, nlist).  grid.y: groups of 8 query
-// blocks (wave w takes blocks 8 y + 2 w and + 1); grid.x: slices of `per`
-// (<= PER_MAX) centroid blocks, which the workgroup stages in LDS (digits,
-// norms, exponents: every load in flight at once) before its waves walk them.
-__global__ __launch_bounds__(256) void k_probe_dots(const int8_t *__restrict__ qdig, const int32_t *__restrict__ qex,
-                                                    int32_t nqc, const int8_t *__restrict__ cdig,
-                                                    const int32_t *__restrict__ cexp, const double *__restrict__ cnorm,
-                                                    int32_t nlist, int32_t per, double *__restrict__ dd) {
-    __shared__ v4i s_dig[PER_MAX * BLK_BYTES / 16];
-    __shared__ double s_cn[PER_MAX * BLK];
-    __shared__ int32_t s_ce[PER_MAX * BLK];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nqb = (nqc + BLK - 1) / BLK;
-    const int qb0 = blockIdx.y * 8 + 2 * w;
-    const bool active = qb0 < nqb, two = qb0 + 1 < nqb;
-    const int ncb = (nlist + BLK - 1) / BLK;
-    const int cb0 = blockIdx.x * per;
-    const int cb1 = min(cb0 + per, ncb);
-
-    v4i a[2][4];
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        a[0][s] = active ? *reinterpret_cast<const v4i *>(qdig + (int64_t)qb0 * BLK_BYTES + s * 1024 + lane * 16)
-                         : v4i{0, 0, 0, 0};
-        a[1][s] = two ? *reinterpret_cast<const v4i *>(qdig + (int64_t)(qb0 + 1) * BLK_BYTES + s * 1024 + lane * 16)
-                      : v4i{0, 0, 0, 0};
-    }
-    {
-        const int nb = cb1 - cb0;
-        const v4i *src = reinterpret_cast<const v4i *>(cdig + (int64_t)cb0 * BLK_BYTES);
-#pragma unroll
-        for (int i = 0; i < PER_MAX; i++)
-            if (i < nb) s_dig[i * 256 + threadIdx.x] = src[i * 256 + threadIdx.x];
-        if (threadIdx.x < nb * BLK) {
-            const int c = cb0 * BLK + threadIdx.x;
-            s_cn[threadIdx.x] = c < nlist ? cnorm[c] : 0.0;
-            s_ce[threadIdx.x] = c < nlist ? cexp[c] : 0;
-        }
-    }
-    __syncthreads();
-    if (!active) return;
-    const bool odd = lane & 1;
-    const int qv = 2 * (lane >> 4) + (lane & 1);  // query within a block
-    const int cv = (lane & 15) >> 1;              // centroid within a block
-    int qe[2];
-    bool qok[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int qi = (qb0 + u) * BLK + qv;
-        qok[u] = qi < nqc;
-        qe[u] = qok[u] ? qex[qi] : 0;
-    }
-
-#pragma unroll 1
-    for (int cb = cb0; cb < cb1; cb++) {
-        const int k = cb - cb0;
-        v4i b[4];
-#pragma unroll
-        for (int s = 0; s < 4; s++) b[s] = s_dig[k * 256 + s * 64 + lane];
-        const double cn = s_cn[k * BLK + cv];
-        const int ce = s_ce[k * BLK + cv];
-        v4i acc[2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            acc[u] = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int s = 0; s < 4; s++) acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u][s], b[s], acc[u], 0, 0, 0);
-        }
-        const int c = cb * BLK + cv;
-        const bool cok = c < nlist;
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            // Lane l holds rows 4 (l/16) .. + 3 (queries 2 (l/16) and + 1, digits
-            // high, low) of column l % 16 (centroid (l%16)/2, digit l % 2).  An
-            // even lane assembles query 2 (l/16), an odd lane query 2 (l/16) + 1.
-            const int32_t s0 = odd ? acc[u][0] : acc[u][2];
-            const int32_t s1 = odd ? acc[u][1] : acc[u][3];
-            const int32_t r0 = __shfl_xor(s0, 1, 64), r1 = __shfl_xor(s1, 1, 64);
-            const int32_t hh = odd ? r0 : acc[u][0];
-            const int32_t lh = odd ? r1 : acc[u][1];
-            const int32_t hl = odd ? acc[u][2] : r0;
-            const int32_t ll = odd ? acc[u][3] : r1;
-            const int64_t dot = (int64_t)hh * 65536 + (int64_t)(hl + lh) * 256 + ll;
-            if (cok && qok[u]) {
-                const int64_t qi = (int64_t)(qb0 + u) * BLK + qv;
-                dd[qi * nlist + c] = cn - ldexp((double)dot, qe[u] + ce + 1);
-            }
-        }
-    }
 }
 
 // Order-preserving map of a float64 onto u64 (finite values; -0 < +0).
@@ -251,179 +186,428 @@ __device__ __forceinline__ void wave_sort_pair(uint64_t &k, int32_t &i, int lane
 
 constexpr uint64_t KNONE = ~0ull;
 constexpr int32_t INONE = 0x7fffffff;
-constexpr int SEL_T = 1024;         // threads per query
-constexpr int SEL_W = SEL_T / 64;   // waves
-constexpr int SEL_J = 12;           // cells per thread and round
-constexpr int SEL_ROUND = SEL_T * SEL_J;
-constexpr int CAND = 1024;          // LDS candidate buffer
 
-// One workgroup of 1024 threads per query q of the chunk: probes[q][0, nprobe)
-// by (dd, id) ascending.  Rounds of 12288 cells: every thread loads its 12
-// values at once; a threshold on the high 32 bits of the ordered keys is the
-// nprobe-th smallest of the 1024 per-thread minima (so at least nprobe
-// candidates lie at or below it, and every member of the top nprobe does);
-// the candidates at or below it (about nprobe of them) and the running top
-// nprobe are collected in LDS and sorted by one wave.  Should the buffer
-// overflow (many equal distances), the round is re-read from memory by
-// nprobe successive minimum searches instead, which is exact for any input.
-__global__ __launch_bounds__(SEL_T) void k_probe_select(const double *__restrict__ dd, int32_t nlist, int32_t nprobe,
-                                                        int32_t *__restrict__ probes) {
-    __shared__ uint64_t s_ck[CAND];
-    __shared__ int32_t s_ci[CAND];
-    __shared__ uint32_t s_lm[SEL_W][PROBE_MAX];
-    __shared__ uint64_t s_bk[PROBE_MAX];
-    __shared__ int32_t s_bi[PROBE_MAX];
-    __shared__ uint32_t s_tau;
-    __shared__ int32_t s_cnt, s_nb;
+// Candidates of (query, slice): the slot of query q (chunk-relative) and slice
+// s holds keys at ck[(q S + s) CAPQ ..] and ids at ci[..], pcnt[q S + s] of them.
+//
+// grid: S * gy workgroups of 256 threads; workgroup b takes (slice, query
+// group) = (idx / gy, idx % gy) with idx dealt so that the gy workgroups of a
+// slice are consecutive on one XCD (workgroup ids go round robin over the 8
+// XCDs), which then reads the slice's digits from HBM once.
+__global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict__ qdig, const int32_t *__restrict__ qex,
+                                                    int32_t nq,
+                                                    const int8_t *__restrict__ cdig, const int32_t *__restrict__ cexp,
+                                                    const double *__restrict__ cnorm, int32_t nlist, int32_t S,
+                                                    int32_t gy, int32_t nprobe, uint64_t *__restrict__ ck,
+                                                    int32_t *__restrict__ ci, int32_t *__restrict__ pcnt) {
+    __shared__ v4i s_b[TPS * TILE_BYTES / 16];
+    __shared__ double s_cn[TPS * TILE];
+    __shared__ int32_t s_ce[TPS * TILE];
+    __shared__ uint32_t s_x[2][4][64][4];  // per (half, query tile, lane, u): minima, then counts
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int64_t q = blockIdx.x;
-    const double *row = dd + q * nlist;
-    if (tid == 0) s_nb = 0;
+    const int qt = w & 3, half = w >> 2;  // query tile; tiles [half HT, half HT + HT) of the slice
+    const int64_t nb = (int64_t)S * gy, b = blockIdx.x;
+    const int64_t idx = nb % 8 == 0 ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int32_t sl = (int32_t)(idx / gy), qg = (int32_t)(idx % gy);
+    const int32_t ntiles = (nlist + TILE - 1) / TILE;
+    const int32_t t0 = sl * TPS, nts = min(TPS, ntiles - t0);
 
-    for (int base = 0; base < nlist; base += SEL_ROUND) {
-        uint64_t key[SEL_J];
+    // The slice's digit tiles, norms and exponents into LDS, every load in flight.
+    {
+        const v4i *src = reinterpret_cast<const v4i *>(cdig + (int64_t)t0 * TILE_BYTES);
+        const int n16 = nts * (TILE_BYTES / 16);
 #pragma unroll
-        for (int j = 0; j < SEL_J; j++) {
-            const int c = base + j * SEL_T + tid;
-            key[j] = c < nlist ? dkey(row[c]) : KNONE;
+        for (int i = 0; i < TPS * TILE_BYTES / 16 / PART_T; i++)
+            if (i * PART_T + tid < n16) s_b[i * PART_T + tid] = src[i * PART_T + tid];
+        if (tid < nts * TILE) {
+            const int32_t c = t0 * TILE + tid;
+            s_cn[tid] = c < nlist ? cnorm[c] : 0.0;
+            s_ce[tid] = c < nlist ? cexp[c] : 0;
         }
-        uint32_t m = 0xffffffffu;
+    }
+
+    // This wave's 16 queries (digit tile qg * 4 + qt of the prepared queries):
+    // lane l holds query (l % 32) / 2, digit l % 2, dims 32 s + 16 (l / 32) ..
+    const int h = lane >> 5, odd = lane & 1;
+    const int q16 = (lane & 31) >> 1;
+    const int32_t qbase = qg * QG + qt * 16;
+    const bool wact = qbase < nq;
+    v4i a[8];
 #pragma unroll
-        for (int j = 0; j < SEL_J; j++) m = min(m, (uint32_t)(key[j] >> 32));
-        const uint32_t ms = wave_sort_u32(m, lane);
-        if (lane < nprobe) s_lm[w][lane] = ms;
-        __syncthreads();  // also orders the previous round's s_bk / s_nb before their use below
-        if (w == 0) {
-            // nprobe-th smallest of the 16 waves' nprobe smallest minima (the
-            // nprobe-th smallest of all 1024), and the running top's bound.
-            uint32_t v[4];
+    for (int s = 0; s < 8; s++)
+        a[s] = wact ? *reinterpret_cast<const v4i *>(qdig + (int64_t)(qbase / TILE) * TILE_BYTES + s * 1024 + lane * 16)
+                    : v4i{0, 0, 0, 0};
+    __syncthreads();
+
+    // Output layout of the 32 x 32 MFMA: lane l holds column l % 32 (centroid
+    // c16 = (l % 32) / 2, digit l % 2) and rows 8 j + 4 h + i (i < 4, j < 4):
+    // queries 4 j + 2 h (rows i = 0, 1: high, low digit) and 4 j + 2 h + 1
+    // (i = 2, 3).  An even lane assembles the queries of blocks j = 0, 1, an
+    // odd lane those of j = 2, 3; the lane's four queries u < 4 are
+    // 4 (2 odd + u / 2) + 2 h + u % 2.
+    const int c16 = q16;
+    int qu[4], qeu[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int e = r * 64 + lane;
-                v[r] = e < SEL_W * nprobe ? s_lm[e / nprobe][e % nprobe] : 0xffffffffu;
+    for (int u = 0; u < 4; u++) {
+        qu[u] = 4 * (2 * odd + u / 2) + 2 * h + (u & 1);
+        qeu[u] = qbase + qu[u] < nq ? qex[qbase + qu[u]] : 0;
+    }
+    // Every tile slot is scored (branch-free): a slot past the slice's tiles
+    // reads stale LDS, and its centroid ids are >= nlist, so its keys are none.
+    uint64_t key[HT][4];
+    uint32_t mn[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+#pragma unroll
+    for (int k0 = 0; k0 < HT; k0++) {
+        const int k = half * HT + k0;
+        {
+            v16i acc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = 0;
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], s_b[k * 512 + s * 64 + lane], acc, 0, 0, 0);
+            // The even lane holds the products with the centroid's high digit,
+            // the odd lane those with its low digit; each sends the other the
+            // eight it needs.
+            // (Selections by a mask, not by ?: on the two elements, which the
+            // compiler would fold into a run-time index into acc.)
+            const int32_t om = -odd;
+            int32_t pch[8], pcl[8];
+#pragma unroll
+            for (int v = 0; v < 8; v++) {
+                const int32_t lo8 = acc[v], hi8 = acc[8 + v];
+                const int32_t own = lo8 ^ ((lo8 ^ hi8) & om);
+                const int32_t got = __shfl_xor(hi8 ^ ((lo8 ^ hi8) & om), 1, 64);
+                pch[v] = own ^ ((own ^ got) & om);
+                pcl[v] = got ^ ((own ^ got) & om);
             }
-            uint32_t t = 0xffffffffu;
+            const int32_t c = (t0 + k) * TILE + c16;
+            const double cn = s_cn[k * TILE + c16];
+            const int ce = s_ce[k * TILE + c16];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int o = 4 * (u / 2) + 2 * (u & 1);
+                const int64_t dot = (int64_t)pch[o] * 65536 + (int64_t)(pcl[o] + pch[o + 1]) * 256 + pcl[o + 1];
+                const double dd = cn - ldexp((double)dot, qeu[u] + ce + 1);
+                key[k0][u] = k < nts && c < nlist ? dkey(dd) : KNONE;
+                mn[u] = min(mn[u], (uint32_t)(key[k0][u] >> 32));
+            }
+        }
+    }
+
+    // Per query, the nprobe-th smallest of its 16 lanes' minima: for a given u
+    // the 16 lanes of an (h, parity) group hold one query, one per centroid
+    // position c16 (lane bits 1..4), so a bitonic sort over c16 by shuffles
+    // puts the r-th smallest in the group's lane c16 = r.
+#pragma unroll
+    for (int u = 0; u < 4; u++) s_x[half][qt][lane][u] = mn[u];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; u++) mn[u] = min(mn[u], s_x[half ^ 1][qt][lane][u]);
+    __syncthreads();
+    uint32_t tau[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        uint32_t x = mn[u];
+#pragma unroll
+        for (int kk = 2; kk <= 16; kk <<= 1) {
+#pragma unroll
+            for (int j = kk >> 1; j > 0; j >>= 1) {
+                const uint32_t y = __shfl_xor(x, 2 * j, 64);
+                const bool take_min = ((c16 & j) == 0) == ((c16 & kk) == 0);
+                x = take_min ? min(x, y) : max(x, y);
+            }
+        }
+        tau[u] = __shfl(x, 32 * h + 2 * (nprobe - 1) + odd, 64);
+    }
+
+    // Candidates: the keys at or below their query's threshold, written at the
+    // count of the group's earlier candidates (a prefix sum over c16), from the
+    // slot's start by the wave of tiles 0 .. HT - 1 and from its end by the
+    // other.  The slot overflows when the two counts exceed CAPQ together.
+    int cnt[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int32_t q = qbase + qu[u];
+        uint32_t pm = 0;
+#pragma unroll
+        for (int k = 0; k < HT; k++) {
+            const uint64_t kk = key[k][u];
+            pm |= (uint32_t)(q < nq && kk != KNONE && (uint32_t)(kk >> 32) <= tau[u]) << k;
+        }
+        const int n = __popc(pm);
+        int incl = n;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const int y = __shfl_up(incl, 2 * d, 64);
+            if (c16 >= d) incl += y;
+        }
+        cnt[u] = __shfl(incl, 32 * h + 30 + odd, 64);
+        int pos = incl - n;
+        uint64_t *sk = ck + ((int64_t)q * S + sl) * CAPQ;
+        int32_t *si = ci + ((int64_t)q * S + sl) * CAPQ;
+#pragma unroll
+        for (int k = 0; k < HT; k++) {
+            if ((pm >> k) & 1) {
+                if (pos < CAPQ) {
+                    const int at = half ? CAPQ - 1 - pos : pos;
+                    sk[at] = key[k][u];
+                    si[at] = (t0 + half * HT + k) * TILE + c16;
+                }
+                pos++;
+            }
+        }
+        s_x[half][qt][lane][u] = (uint32_t)cnt[u];
+    }
+    __syncthreads();
+    bool over = false;
+    bool ov[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        ov[u] = cnt[u] + (int)s_x[half ^ 1][qt][lane][u] > CAPQ;
+        over |= ov[u];
+    }
+
+    // A slot that overflowed gets each half's exact top nprobe instead (at the
+    // slot's two ends): nprobe successive minima by (key, id) over the group's
+    // registers, strictly above the last one taken (the four groups of a u at
+    // once).
+    if (__ballot(over)) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const bool mine = ov[u];
+            if (!__ballot(mine)) continue;
+            const int32_t q = qbase + qu[u];
+            uint64_t *sk = ck + ((int64_t)q * S + sl) * CAPQ;
+            int32_t *si = ci + ((int64_t)q * S + sl) * CAPQ;
+            uint64_t lk = 0;
+            int32_t li = -1;
+            int found = 0;
             for (int r = 0; r < nprobe; r++) {
-                uint32_t lm = min(min(v[0], v[1]), min(v[2], v[3]));
-                uint32_t wm = lm;
+                uint64_t bk = KNONE;
+                int32_t bi = INONE;
 #pragma unroll
-                for (int o = 1; o < 64; o <<= 1) wm = min(wm, __shfl_xor(wm, o, 64));
-                t = wm;
-                // The lowest lane holding wm drops one copy of it.
-                const uint64_t holders = __ballot(lm == wm);
-                if (lane == __builtin_ctzll(holders)) {
-                    if (v[0] == wm) v[0] = 0xffffffffu;
-                    else if (v[1] == wm) v[1] = 0xffffffffu;
-                    else if (v[2] == wm) v[2] = 0xffffffffu;
-                    else v[3] = 0xffffffffu;
-                }
-            }
-            const int nb = s_nb;
-            if (nb == nprobe) t = min(t, (uint32_t)(s_bk[nprobe - 1] >> 32));
-            if (lane == 0) {
-                s_tau = t;
-                s_cnt = nb;
-            }
-            if (lane < nb) {  // the running top nprobe are candidates too
-                s_ck[lane] = s_bk[lane];
-                s_ci[lane] = s_bi[lane];
-            }
-        }
-        __syncthreads();
-        const uint32_t tau = s_tau;
-        int npass = 0;
-#pragma unroll
-        for (int j = 0; j < SEL_J; j++) npass += __popcll(__ballot((uint32_t)(key[j] >> 32) <= tau && key[j] != KNONE));
-        int off = 0;
-        if (lane == 0 && npass) off = atomicAdd(&s_cnt, npass);
-        off = __shfl(off, 0, 64);
-#pragma unroll
-        for (int j = 0; j < SEL_J; j++) {
-            const bool pass = (uint32_t)(key[j] >> 32) <= tau && key[j] != KNONE;
-            const uint64_t bal = __ballot(pass);
-            const int pos = off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-            if (pass && pos < CAND) {
-                s_ck[pos] = key[j];
-                s_ci[pos] = base + j * SEL_T + tid;
-            }
-            off += __popcll(bal);
-        }
-        __syncthreads();
-        if (w == 0) {
-            const int cnt = s_cnt;
-            int nb = 0;
-            if (cnt <= 64) {
-                uint64_t k = lane < cnt ? s_ck[lane] : KNONE;
-                int32_t i = lane < cnt ? s_ci[lane] : INONE;
-                wave_sort_pair(k, i, lane);
-                nb = min(cnt, nprobe);
-                if (lane < nb) {
-                    s_bk[lane] = k;
-                    s_bi[lane] = i;
-                }
-            } else {
-                // nprobe successive minima strictly above the last one taken
-                // (the pairs are distinct): over the buffer, or, if it
-                // overflowed, over the round's cells and the running top.
-                const bool over = cnt > CAND;
-                const int nbo = s_nb;
-                const uint64_t tk = lane < nbo ? s_bk[lane] : KNONE;  // the running top, read before it is replaced
-                const int32_t ti = lane < nbo ? s_bi[lane] : INONE;
-                uint64_t lk = 0, rk = KNONE;
-                int32_t li = -1, ri = INONE;
-                const int end = min(nlist - base, SEL_ROUND);
-                for (int r = 0; r < nprobe; r++) {
-                    uint64_t bk = KNONE;
-                    int32_t bi = INONE;
-                    if (!over) {
-                        for (int e = lane; e < cnt; e += 64) {
-                            const uint64_t k = s_ck[e];
-                            const int32_t i = s_ci[e];
-                            if (lt(lk, li, k, i) && lt(k, i, bk, bi)) {
-                                bk = k;
-                                bi = i;
-                            }
-                        }
-                    } else {
-                        for (int e = lane; e < end; e += 64) {
-                            const uint64_t k = dkey(row[base + e]);
-                            const int32_t i = base + e;
-                            if (lt(lk, li, k, i) && lt(k, i, bk, bi)) {
-                                bk = k;
-                                bi = i;
-                            }
-                        }
-                        if (lt(lk, li, tk, ti) && lt(tk, ti, bk, bi)) {
-                            bk = tk;
-                            bi = ti;
-                        }
+                for (int k = 0; k < HT; k++) {
+                    const uint64_t kk = key[k][u];
+                    const int32_t id = (t0 + half * HT + k) * TILE + c16;
+                    if (kk != KNONE && lt(lk, li, kk, id) && lt(kk, id, bk, bi)) {
+                        bk = kk;
+                        bi = id;
                     }
-                    wave_min(bk, bi);
-                    if (bk == KNONE && bi == INONE) break;
-                    if (lane == r) {
-                        rk = bk;
-                        ri = bi;
+                }
+#pragma unroll
+                for (int d = 2; d < 32; d <<= 1) {  // minimum over the group (lane bits 1..4)
+                    const uint64_t ko = shfl_xor_u64(bk, d);
+                    const int32_t io = __shfl_xor(bi, d, 64);
+                    if (lt(ko, io, bk, bi)) {
+                        bk = ko;
+                        bi = io;
+                    }
+                }
+                if (!(bk == KNONE && bi == INONE)) {
+                    if (mine && c16 == 0) {
+                        const int at = half ? CAPQ - 1 - r : r;
+                        sk[at] = bk;
+                        si[at] = bi;
                     }
                     lk = bk;
                     li = bi;
-                    nb = r + 1;
-                }
-                if (lane < nb) {
-                    s_bk[lane] = rk;
-                    s_bi[lane] = ri;
+                    found = r + 1;
                 }
             }
-            if (lane == 0) s_nb = nb;
+            if (mine) cnt[u] = found;
         }
     }
     __syncthreads();
-    if (tid < nprobe) probes[q * nprobe + tid] = tid < s_nb ? s_bi[tid] : -1;
+#pragma unroll
+    for (int u = 0; u < 4; u++) s_x[half][qt][lane][u] = (uint32_t)min(cnt[u], CAPQ);
+    __syncthreads();
+    // The slot's count: low 16 bits from its start, high 16 bits from its end.
+    if (half == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int32_t q = qbase + qu[u];
+            if (c16 == 0 && q < nq)
+                pcnt[(int64_t)q * S + sl] = (int32_t)(s_x[0][qt][lane][u] | (s_x[1][qt][lane][u] << 16));
+        }
+    }
+}
+
+// Entry e of a slot whose count word is c: the first (c & 0xffff) entries
+// from the slot's start, then (c >> 16) from its end; -1 past them.
+__device__ __forceinline__ int slot_entry(int32_t c, int e) {
+    const int na = c & 0xffff, nb = (c >> 16) & 0xffff;
+    return e < na ? e : e - na < nb ? CAPQ - 1 - (e - na) : -1;
+}
+
+__device__ __forceinline__ int slot_size(int32_t c) { return (c & 0xffff) + ((c >> 16) & 0xffff); }
+
+constexpr int MREG = 24;  // candidates per lane held in registers by the merge
+
+// Four queries per workgroup, one wave each: probes[q][0, nprobe) by (key, id)
+// ascending over the candidates of its S slots (lane l takes slots l, l + 64,
+// ..).  A threshold on the high 32 bits of the keys is the nprobe-th smallest
+// of the 64 lanes' minima, so at least nprobe candidates lie at or below it
+// and every member of the top nprobe does; those (about nprobe) are gathered
+// in LDS and sorted by the wave.  More than 64 of them (equal or near-equal
+// distances) switch to nprobe successive minimum searches over all the
+// candidates, which is exact for any input.
+__global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict__ ck, const int32_t *__restrict__ ci,
+                                                     const int32_t *__restrict__ pcnt, int32_t nqc, int32_t S,
+                                                     int32_t nprobe, int32_t *__restrict__ probes) {
+    __shared__ uint64_t s_k[4][64];
+    __shared__ int32_t s_i[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t q = (int64_t)blockIdx.x * 4 + w;
+    if (q >= nqc) return;
+    const uint64_t *qk = ck + q * S * CAPQ;
+    const int32_t *qi = ci + q * S * CAPQ;
+    const int32_t *qc = pcnt + q * S;
+    uint64_t *wk = s_k[w];
+    int32_t *wi = s_i[w];
+
+    // Gathers the candidates at or below tau (there are `total`, at most 64)
+    // into the wave's LDS rows, lane `pos` onwards, then sorts them.
+    auto finish = [&](uint64_t k, int32_t id, int total) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS stores are done
+        __builtin_amdgcn_wave_barrier();
+        k = lane < total ? wk[lane] : KNONE;
+        id = lane < total ? wi[lane] : INONE;
+        wave_sort_pair(k, id, lane);
+        if (lane < nprobe) probes[q * nprobe + lane] = lane < total ? id : -1;
+    };
+
+    // One slot per lane holding at most MREG candidates (the usual case): one
+    // round of loads into registers, then the selection from them.
+    const int32_t c0 = lane < S ? qc[lane] : 0;
+    if (S <= 64 && !__ballot(slot_size(c0) > MREG)) {
+        uint64_t kk[MREG];
+        int32_t ii[MREG];
+#pragma unroll
+        for (int e = 0; e < MREG; e++) {
+            const int at = slot_entry(c0, e);
+            kk[e] = at >= 0 ? qk[(int64_t)lane * CAPQ + at] : KNONE;
+            ii[e] = at >= 0 ? qi[(int64_t)lane * CAPQ + at] : INONE;
+        }
+        uint32_t m = 0xffffffffu;
+#pragma unroll
+        for (int e = 0; e < MREG; e++) m = min(m, (uint32_t)(kk[e] >> 32));
+        const uint32_t tau = __shfl(wave_sort_u32(m, lane), nprobe - 1, 64);
+        uint32_t pm = 0;
+#pragma unroll
+        for (int e = 0; e < MREG; e++) pm |= (uint32_t)(kk[e] != KNONE && (uint32_t)(kk[e] >> 32) <= tau) << e;
+        const int mine = __popc(pm);
+        int incl = mine;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        const int total = __shfl(incl, 63, 64);
+        if (total <= 64) {
+            int pos = incl - mine;
+#pragma unroll
+            for (int e = 0; e < MREG; e++) {
+                if ((pm >> e) & 1) {
+                    wk[pos] = kk[e];
+                    wi[pos] = ii[e];
+                    pos++;
+                }
+            }
+            finish(0, 0, total);
+            return;
+        }
+        uint64_t lk = 0;
+        int32_t li = -1;
+        int32_t res = -1;
+        for (int r = 0; r < nprobe; r++) {
+            uint64_t bk = KNONE;
+            int32_t bi = INONE;
+#pragma unroll
+            for (int e = 0; e < MREG; e++) {
+                if (kk[e] != KNONE && lt(lk, li, kk[e], ii[e]) && lt(kk[e], ii[e], bk, bi)) {
+                    bk = kk[e];
+                    bi = ii[e];
+                }
+            }
+            wave_min(bk, bi);
+            if (bk == KNONE && bi == INONE) break;
+            if (lane == r) res = bi;
+            lk = bk;
+            li = bi;
+        }
+        if (lane < nprobe) probes[q * nprobe + lane] = res;
+        return;
+    }
+
+    // Any slot count and layout: the same selection, re-reading the slots.
+    uint32_t m = 0xffffffffu;
+    for (int32_t sl = lane; sl < S; sl += 64) {
+        const int32_t c = qc[sl];
+        for (int e = 0; e < slot_size(c); e++) m = min(m, (uint32_t)(qk[(int64_t)sl * CAPQ + slot_entry(c, e)] >> 32));
+    }
+    const uint32_t tau = __shfl(wave_sort_u32(m, lane), nprobe - 1, 64);
+    int mine = 0;
+    for (int32_t sl = lane; sl < S; sl += 64) {
+        const int32_t c = qc[sl];
+        for (int e = 0; e < slot_size(c); e++)
+            mine += (uint32_t)(qk[(int64_t)sl * CAPQ + slot_entry(c, e)] >> 32) <= tau;
+    }
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    const int total = __shfl(incl, 63, 64);
+    if (total <= 64) {
+        int pos = incl - mine;
+        for (int32_t sl = lane; sl < S; sl += 64) {
+            const int32_t c = qc[sl];
+            for (int e = 0; e < slot_size(c); e++) {
+                const int64_t at = (int64_t)sl * CAPQ + slot_entry(c, e);
+                const uint64_t kk = qk[at];
+                if ((uint32_t)(kk >> 32) <= tau) {
+                    wk[pos] = kk;
+                    wi[pos] = qi[at];
+                    pos++;
+                }
+            }
+        }
+        finish(0, 0, total);
+        return;
+    }
+    uint64_t lk = 0;
+    int32_t li = -1;
+    int32_t res = -1;
+    for (int r = 0; r < nprobe; r++) {
+        uint64_t bk = KNONE;
+        int32_t bi = INONE;
+        for (int32_t sl = lane; sl < S; sl += 64) {
+            const int32_t c = qc[sl];
+            for (int e = 0; e < slot_size(c); e++) {
+                const int64_t at = (int64_t)sl * CAPQ + slot_entry(c, e);
+                const uint64_t kk = qk[at];
+                const int32_t ii = qi[at];
+                if (lt(lk, li, kk, ii) && lt(kk, ii, bk, bi)) {
+                    bk = kk;
+                    bi = ii;
+                }
+            }
+        }
+        wave_min(bk, bi);
+        if (bk == KNONE && bi == INONE) break;
+        if (lane == r) res = bi;
+        lk = bk;
+        li = bi;
+    }
+    if (lane < nprobe) probes[q * nprobe + lane] = res;
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 st_status launch_prep(const float *x, int64_t n, int8_t *dig, int32_t *ex, double *norm, hipStream_t s) {
-    const int64_t rows = cdiv(n, BLK) * BLK;
+    const int64_t rows = cdiv(n, TILE) * TILE;
     hipLaunchKernelGGL(k_probe_prep, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, x, n, dig, ex, norm);
     ST_LAUNCH_CHECK();
     return ST_OK;
@@ -433,7 +617,7 @@ st_status launch_prep(const float *x, int64_t n, int8_t *dig, int32_t *ex, doubl
 
 extern "C" int64_t st_knn_centroid_digit_bytes(int64_t nlist, int64_t d) {
     if (nlist < 0 || d != D) return -1;
-    return cdiv(nlist, BLK) * BLK_BYTES;
+    return cdiv(nlist, TILE) * TILE_BYTES;
 }
 
 extern "C" st_status st_knn_centroids_prep(const float *centroids, int64_t nlist, int64_t d, int8_t *digits,
@@ -441,8 +625,8 @@ extern "C" st_status st_knn_centroids_prep(const float *centroids, int64_t nlist
     st::clear_error();
     if (!centroids || !digits || !cexp || !cnorm) return st::fail(ST_ERR_INVALID, "centroids_prep: NULL buffer");
     if (d != D) return st::fail(ST_ERR_INVALID, "centroids_prep: built for d == %d (got %lld)", D, (long long)d);
-    if (nlist < 1 || nlist > INT32_MAX - BLK)
-        return st::fail(ST_ERR_INVALID, "centroids_prep: nlist must be in 1..2^31 - 9 (got %lld)", (long long)nlist);
+    if (nlist < 1 || nlist > INT32_MAX / 2)
+        return st::fail(ST_ERR_INVALID, "centroids_prep: nlist must be in 1..2^30 (got %lld)", (long long)nlist);
     if ((reinterpret_cast<uintptr_t>(centroids) & 15) != 0 || (reinterpret_cast<uintptr_t>(digits) & 15) != 0)
         return st::fail(ST_ERR_INVALID, "centroids_prep: centroids and digits must be 16-byte aligned");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
@@ -455,7 +639,7 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
     st::clear_error();
     if (!digits || !cexp || !cnorm || !queries || !probes) return st::fail(ST_ERR_INVALID, "probe: NULL buffer");
     if (d != D) return st::fail(ST_ERR_INVALID, "probe: built for d == %d (got %lld)", D, (long long)d);
-    if (nlist < 1 || nlist > INT32_MAX - BLK || nq < 0)
+    if (nlist < 1 || nlist > INT32_MAX / 2 || nq < 0)
         return st::fail(ST_ERR_INVALID, "probe: bad nlist or nq");
     if (nprobe < 1 || nprobe > nlist || nprobe > PROBE_MAX)
         return st::fail(ST_ERR_INVALID, "probe: nprobe must be in 1..=min(nlist, %d) (got %lld)", PROBE_MAX,
@@ -466,33 +650,33 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     const hipStream_t s = st::stream_of(stream);
 
-    // Queries in chunks whose dd matrix fits DD_BUDGET (multiples of 64 queries).
-    int64_t chunk = DD_BUDGET / (nlist * (int64_t)sizeof(double));
-    chunk = chunk < 64 ? 64 : chunk / 64 * 64;
-    if (chunk > nq) chunk = cdiv(nq, BLK) * BLK;
-    const int64_t dd_bytes = chunk * nlist * (int64_t)sizeof(double);
-    const int64_t dig_bytes = cdiv(chunk, BLK) * BLK_BYTES;
-    char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, (size_t)(dd_bytes + dig_bytes + chunk * 4), s));
+    // Queries in chunks (multiples of 64) whose candidate slots fit CAND_BUDGET.
+    const int64_t ntiles = cdiv(nlist, TILE), S = cdiv(ntiles, TPS);
+    const int64_t per_q = S * CAPQ * (int64_t)(sizeof(uint64_t) + sizeof(int32_t)) + S * (int64_t)sizeof(int32_t) +
+                          2 * D + (int64_t)sizeof(int32_t);
+    int64_t chunk = CAND_BUDGET / per_q;
+    chunk = chunk < QG ? QG : chunk / QG * QG;
+    if (chunk > nq) chunk = cdiv(nq, QG) * QG;
+    if (S * cdiv(chunk, QG) > INT32_MAX) return st::fail(ST_ERR_INVALID, "probe: too many centroids");
+    char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, (size_t)(chunk * per_q), s));
     if (!base) return st::scratch_status();
-    double *dd = reinterpret_cast<double *>(base);
-    int8_t *qdig = reinterpret_cast<int8_t *>(base + dd_bytes);
-    int32_t *qex = reinterpret_cast<int32_t *>(base + dd_bytes + dig_bytes);
+    // [query digit tiles][candidate keys][candidate ids][counts][query exponents]
+    int8_t *qdig = reinterpret_cast<int8_t *>(base);
+    uint64_t *ck = reinterpret_cast<uint64_t *>(base + chunk * 2 * D);
+    int32_t *ci = reinterpret_cast<int32_t *>(ck + chunk * S * CAPQ);
+    int32_t *pcnt = ci + chunk * S * CAPQ;
+    int32_t *qex = pcnt + chunk * S;
 
-    const int64_t ncb = cdiv(nlist, BLK);
     for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
         const int64_t nqc = nq - q0 < chunk ? nq - q0 : chunk;
+        const int64_t gy = cdiv(nqc, QG);
         st_status st = launch_prep(queries + q0 * D, nqc, qdig, qex, nullptr, s);
         if (st != ST_OK) return st;
-        const int64_t gy = cdiv(cdiv(nqc, BLK), 8);
-        int64_t per = cdiv(ncb * gy, 1024);
-        if (per < 2) per = 2;
-        if (per > PER_MAX) per = PER_MAX;
-        const int64_t gx = cdiv(ncb, per);
-        hipLaunchKernelGGL(k_probe_dots, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, qdig, qex, (int32_t)nqc,
-                           digits, cexp, cnorm, (int32_t)nlist, (int32_t)per, dd);
+        hipLaunchKernelGGL(k_probe_part, dim3((unsigned)(S * gy)), dim3(PART_T), 0, s, qdig, qex, (int32_t)nqc, digits,
+                           cexp, cnorm, (int32_t)nlist, (int32_t)S, (int32_t)gy, (int32_t)nprobe, ck, ci, pcnt);
         ST_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_probe_select, dim3((unsigned)nqc), dim3(SEL_T), 0, s, dd, (int32_t)nlist, (int32_t)nprobe,
-                           probes + q0 * nprobe);
+        hipLaunchKernelGGL(k_probe_merge, dim3((unsigned)cdiv(nqc, 4)), dim3(256), 0, s, ck, ci, pcnt, (int32_t)nqc,
+                           (int32_t)S, (int32_t)nprobe, probes + q0 * nprobe);
         ST_LAUNCH_CHECK();
     }
     return ST_OK;
