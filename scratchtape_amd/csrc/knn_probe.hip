@@ -188,7 +188,9 @@ constexpr uint64_t KNONE = ~0ull;
 constexpr int32_t INONE = 0x7fffffff;
 
 // Candidates of (query, slice): the slot of query q (chunk-relative) and slice
-// s holds keys at ck[(q S + s) CAPQ ..] and ids at ci[..], pcnt[q S + s] of them.
+// s keeps entry e at ck[(q CAPQ + e) S + s] (keys) and ci[..] (ids), so that a
+// lane per slot reads an entry of consecutive slots with one coalesced load;
+// pcnt[q S + s] counts them.
 //
 // grid: S * gy workgroups of 256 threads; workgroup b takes (slice, query
 // group) = (idx / gy, idx % gy) with idx dealt so that the gy workgroups of a
@@ -260,12 +262,21 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
     for (int k0 = 0; k0 < HT; k0++) {
         const int k = half * HT + k0;
         {
-            v16i acc;
+            // Two accumulator chains (k-steps 0..3 and 4..7) halve the MFMA
+            // dependency chain; their sum is exact.
+            v16i acc, acc2;
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] = 0;
+            for (int i = 0; i < 16; i++) {
+                acc[i] = 0;
+                acc2[i] = 0;
+            }
 #pragma unroll
-            for (int s = 0; s < 8; s++)
+            for (int s = 0; s < 4; s++) {
                 acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], s_b[k * 512 + s * 64 + lane], acc, 0, 0, 0);
+                acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s + 4], s_b[k * 512 + (s + 4) * 64 + lane], acc2, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] += acc2[i];
             // The even lane holds the products with the centroid's high digit,
             // the odd lane those with its low digit; each sends the other the
             // eight it needs.
@@ -344,13 +355,13 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
         }
         cnt[u] = __shfl(incl, 32 * h + 30 + odd, 64);
         int pos = incl - n;
-        uint64_t *sk = ck + ((int64_t)q * S + sl) * CAPQ;
-        int32_t *si = ci + ((int64_t)q * S + sl) * CAPQ;
+        uint64_t *sk = ck + (int64_t)q * S * CAPQ + sl;
+        int32_t *si = ci + (int64_t)q * S * CAPQ + sl;
 #pragma unroll
         for (int k = 0; k < HT; k++) {
             if ((pm >> k) & 1) {
                 if (pos < CAPQ) {
-                    const int at = half ? CAPQ - 1 - pos : pos;
+                    const int64_t at = (int64_t)(half ? CAPQ - 1 - pos : pos) * S;
                     sk[at] = key[k][u];
                     si[at] = (t0 + half * HT + k) * TILE + c16;
                 }
@@ -378,8 +389,8 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
             const bool mine = ov[u];
             if (!__ballot(mine)) continue;
             const int32_t q = qbase + qu[u];
-            uint64_t *sk = ck + ((int64_t)q * S + sl) * CAPQ;
-            int32_t *si = ci + ((int64_t)q * S + sl) * CAPQ;
+            uint64_t *sk = ck + (int64_t)q * S * CAPQ + sl;
+            int32_t *si = ci + (int64_t)q * S * CAPQ + sl;
             uint64_t lk = 0;
             int32_t li = -1;
             int found = 0;
@@ -406,7 +417,7 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
                 }
                 if (!(bk == KNONE && bi == INONE)) {
                     if (mine && c16 == 0) {
-                        const int at = half ? CAPQ - 1 - r : r;
+                        const int64_t at = (int64_t)(half ? CAPQ - 1 - r : r) * S;
                         sk[at] = bk;
                         si[at] = bi;
                     }
@@ -477,17 +488,29 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
         if (lane < nprobe) probes[q * nprobe + lane] = lane < total ? id : -1;
     };
 
-    // One slot per lane holding at most MREG candidates (the usual case): one
-    // round of loads into registers, then the selection from them.
+    // One slot per lane with at most MREG / 2 candidates at either end (the
+    // usual case): the ends' entries are loaded with the count, not after it
+    // (each load one coalesced row of the slots), then selected from registers.
     const int32_t c0 = lane < S ? qc[lane] : 0;
-    if (S <= 64 && !__ballot(slot_size(c0) > MREG)) {
-        uint64_t kk[MREG];
-        int32_t ii[MREG];
+    uint64_t kk[MREG];
+    int32_t ii[MREG];
+    if (S <= 64) {
 #pragma unroll
         for (int e = 0; e < MREG; e++) {
-            const int at = slot_entry(c0, e);
-            kk[e] = at >= 0 ? qk[(int64_t)lane * CAPQ + at] : KNONE;
-            ii[e] = at >= 0 ? qi[(int64_t)lane * CAPQ + at] : INONE;
+            const int at = e < MREG / 2 ? e : CAPQ - 1 - (e - MREG / 2);
+            kk[e] = lane < S ? qk[(int64_t)at * S + lane] : KNONE;
+            ii[e] = lane < S ? qi[(int64_t)at * S + lane] : INONE;
+        }
+    }
+    const int ca = c0 & 0xffff, cb = (c0 >> 16) & 0xffff;
+    if (S <= 64 && !__ballot(ca > MREG / 2 || cb > MREG / 2)) {
+#pragma unroll
+        for (int e = 0; e < MREG; e++) {
+            const bool valid = e < MREG / 2 ? e < ca : e - MREG / 2 < cb;
+            if (!valid) {
+                kk[e] = KNONE;
+                ii[e] = INONE;
+            }
         }
         uint32_t m = 0xffffffffu;
 #pragma unroll
@@ -544,14 +567,14 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
     uint32_t m = 0xffffffffu;
     for (int32_t sl = lane; sl < S; sl += 64) {
         const int32_t c = qc[sl];
-        for (int e = 0; e < slot_size(c); e++) m = min(m, (uint32_t)(qk[(int64_t)sl * CAPQ + slot_entry(c, e)] >> 32));
+        for (int e = 0; e < slot_size(c); e++) m = min(m, (uint32_t)(qk[(int64_t)slot_entry(c, e) * S + sl] >> 32));
     }
     const uint32_t tau = __shfl(wave_sort_u32(m, lane), nprobe - 1, 64);
     int mine = 0;
     for (int32_t sl = lane; sl < S; sl += 64) {
         const int32_t c = qc[sl];
         for (int e = 0; e < slot_size(c); e++)
-            mine += (uint32_t)(qk[(int64_t)sl * CAPQ + slot_entry(c, e)] >> 32) <= tau;
+            mine += (uint32_t)(qk[(int64_t)slot_entry(c, e) * S + sl] >> 32) <= tau;
     }
     int incl = mine;
 #pragma unroll
@@ -565,7 +588,7 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
         for (int32_t sl = lane; sl < S; sl += 64) {
             const int32_t c = qc[sl];
             for (int e = 0; e < slot_size(c); e++) {
-                const int64_t at = (int64_t)sl * CAPQ + slot_entry(c, e);
+                const int64_t at = (int64_t)slot_entry(c, e) * S + sl;
                 const uint64_t kk = qk[at];
                 if ((uint32_t)(kk >> 32) <= tau) {
                     wk[pos] = kk;
@@ -586,7 +609,7 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
         for (int32_t sl = lane; sl < S; sl += 64) {
             const int32_t c = qc[sl];
             for (int e = 0; e < slot_size(c); e++) {
-                const int64_t at = (int64_t)sl * CAPQ + slot_entry(c, e);
+                const int64_t at = (int64_t)slot_entry(c, e) * S + sl;
                 const uint64_t kk = qk[at];
                 const int32_t ii = qi[at];
                 if (lt(lk, li, kk, ii) && lt(kk, ii, bk, bi)) {
