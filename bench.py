@@ -479,7 +479,7 @@ def bench_layer_norm(dev, stream, steps, warmup):
     nbytes = 4 * (5 * n * d + 4 * n)
     return dict(rows=n, d=d, fwd_ms=round(fwd_ms, 5), graph_per_step_ms=round(per_step_ms, 5),
                 graph_ms=round(graph_ms, 5),
-                roofline=roofline("k_ln_fwd + k_ln_bwd_dx + k_ln_bwd_part + k_ln_bwd_sum", 10 * n * d, nbytes,
+                roofline=roofline("k_ln_fwd4 + k_ln_bwd4 + k_ln_bwd_sum4", 10 * n * d, nbytes,
                                   graph_ms, traffic_for("k_ln step", "scratchtape_amd/csrc/rows.hip"), route="f32"))
 
 
