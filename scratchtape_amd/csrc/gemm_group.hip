@@ -462,10 +462,27 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 // 4 groups per wave) and the transposed writes (rows W l + w, one group) each
 // touch every bank once per 16 lanes (64 banks) and per 8 lanes (32 banks).
 //
-// One barrier per stage: stage q is multiplied from slot q % 3 while stage
-// q + 1 is converted into slot (q + 1) % 3 and the loads of stages q + 2 and
-// q + 3 are in flight (three register sets).
+// Stage q is multiplied from slot q % 3 while stage q + 1 is converted into
+// slot (q + 1) % 3 and the loads of stages q + 2 and q + 3 are in flight
+// (three register sets).  The roles hand slots over through two counters per
+// slot in LDS instead of a workgroup barrier per stage: each producer wave
+// adds 1 to full[s] once its part of a stage is written, each consumer wave
+// adds 1 to empty[s] once it has read its fragments, and a wave waits only
+// for the counter it needs (the consumers for full[s] to reach 4 (u + 1) for
+// the u-th use of slot s, the producers for empty[s] to reach 4 u before
+// writing it).  So neither role waits for the other's whole step: producers
+// keep loading and converting through the consumers' epilogues, up to two
+// stages ahead.
 namespace r16 {
+
+// Waits until the LDS counter reaches target (bounded, so that a wave always
+// ends; the protocol reaches every target).
+__device__ __forceinline__ void spin_until(uint32_t *p, uint32_t target) {
+    for (int i = 0; i < (1 << 20); i++) {
+        if (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
 
 constexpr int NSL = 3;  // LDS slots = producer register sets
 
@@ -651,8 +668,9 @@ template <class C>
 __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
     constexpr int TM = C::TM, SA = C::SA, SLOT = C::SLOT;
     constexpr int WM = C::WM, M32 = C::M32, N32 = C::N32;
-    __shared__ __attribute__((aligned(16))) char lds[NSL * SLOT];
-    __shared__ float csp[NSL][4][TN];  // column-sum partials of B per stage slot and k-group
+    __shared__ __attribute__((aligned(16))) char lds[(NSL + 1) * SLOT];  // + a slot for the last, unused conversion
+    __shared__ float csp[NSL + 1][4][TN];  // column-sum partials of B per stage slot and k-group
+    __shared__ uint32_t s_full[NSL], s_empty[NSL];
     __shared__ GroupArgs sga;
     __shared__ int32_t cum[st::GROUP_MAX + 1];
 
@@ -662,6 +680,10 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
     const int wm = (wave >> 1) & 1, wn = wave & 1;
     const int x = blockIdx.x % XCDS, L = gridDim.x / XCDS;
     const int w = blockIdx.x / XCDS;
+    if (tid < NSL) {
+        s_full[tid] = 0;
+        s_empty[tid] = 0;
+    }
     load_args(ga, sga, cum, x, tid, C::THREADS);
 
     const int nlist = uni(cum[sga.count]), sched = uni(sga.sched);
@@ -719,12 +741,14 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         constexpr int S = decltype(set_c)::value;
         const int s = st + ahead;
         const bool in_cur = s < cur.nst, none = !in_cur && nxt.p < 0;
-        // Past the last stage the dummy loads are converted too, into a slot
-        // nobody reads again: every register set is waited for on every path.
+        // Past the last stage the dummy loads are converted too, into the
+        // extra slot NSL that nobody reads: every register set is waited for
+        // on every path, and no slot the consumers still read is written.
         const bool akc = in_cur || none ? cur.a.kc : nxt.a.kc, bkc = in_cur || none ? cur.b.kc : nxt.b.kc;
         const bool cs = !none && (in_cur ? cur.cs : nxt.cs);
-        store_op<TM>(va[S], akc, lds + S * SLOT, id);
-        store_op<TN>(vb[S], bkc, lds + S * SLOT + SA, id);
+        const int P = none ? NSL : S;
+        store_op<TM>(va[S], akc, lds + P * SLOT, id);
+        store_op<TN>(vb[S], bkc, lds + P * SLOT + SA, id);
         if (cs) {
             // B is row-contiguous here (the f16 route sums columns only then):
             // this lane holds columns 2 (id % 64) + w2 on k 8 (id / 64) .. + 7.
@@ -733,7 +757,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
                 float p = 0.f;
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) p += f_(vb[S][jj][w2]);
-                csp[S][id >> 6][2 * (id & 63) + w2] = p;
+                csp[P][id >> 6][2 * (id & 63) + w2] = p;
             }
         }
     };
@@ -758,13 +782,6 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][n][e] = 0.f;
     float cs_acc = 0.f;  // column col0 + id of B summed over this unit's k (consumers, id < 128)
-
-    auto lds_fence_bar = [&]() __attribute__((always_inline)) {
-        // this wave's LDS writes done (vector-memory loads stay in flight),
-        // then the workgroup barrier
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        bar();
-    };
 
     // The epilogue of cur, straight from the accumulators: lane l holds
     // column l % 32 of each 32 x 32 block and rows 8 (e / 4) + 4 (l / 32) +
@@ -849,14 +866,16 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
     };
 
     // The two roles run separate loops (so their registers never live at the
-    // same time) with the same barriers: one per stage, plus the prologue's.
+    // same time), joined only by the slot counters.
     if (producer) {
         // Prologue: stages 0, 1, 2 of cur in flight; stage 0 into slot 0.
         issue(std::integral_constant<int, 0>());
         issue(std::integral_constant<int, 1>());
         issue(std::integral_constant<int, 2>());
         convert(std::integral_constant<int, 0>(), 0);
-        lds_fence_bar();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are done
+        if (lane == 0) __hip_atomic_fetch_add(&s_full[0], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t pc = 1;  // stages converted so far (over the workgroup's units)
         // Stage q (slot S): load stage q + 3 into register set S, convert
         // stage q + 1 into slot S + 1.
         auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
@@ -866,37 +885,48 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
             // cannot work out through the loop's back edge by itself.
             wait_vm<32>();
             issue(set_c);
-            convert(std::integral_constant<int, (S + 1) % NSL>(), 1);
-            lds_fence_bar();
+            constexpr int S1 = (S + 1) % NSL;
+            const bool none = !(st + 1 < cur.nst) && nxt.p < 0;
+            if (!none) spin_until(&s_empty[S1], 4 * (pc / NSL));
+            convert(std::integral_constant<int, S1>(), 1);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            if (!none && lane == 0)
+                __hip_atomic_fetch_add(&s_full[S1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            pc++;
             return ++st < cur.nst || advance();
         };
         while (step(std::integral_constant<int, 0>()) && step(std::integral_constant<int, 1>()) &&
                step(std::integral_constant<int, 2>())) {
         }
     } else {
-        lds_fence_bar();
+        uint32_t cq = 0;  // stages consumed so far
         // Stage q: multiply slot S.
         auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
             constexpr int S = decltype(set_c)::value;
+            spin_until(&s_full[S], 4 * (cq / NSL + 1));
             const char *slot = lds + S * SLOT;
+            half8 af[2][M32], bf[2][N32];
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                half8 af[M32], bf[N32];
 #pragma unroll
-                for (int i = 0; i < M32; i++) af[i] = *reinterpret_cast<const half8 *>(slot + ra[i][ks]);
+                for (int i = 0; i < M32; i++) af[ks][i] = *reinterpret_cast<const half8 *>(slot + ra[i][ks]);
 #pragma unroll
-                for (int n = 0; n < N32; n++) bf[n] = *reinterpret_cast<const half8 *>(slot + rb[n][ks]);
-#pragma unroll
-                for (int i = 0; i < M32; i++)
-#pragma unroll
-                    for (int n = 0; n < N32; n++)
-                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[n], acc[i][n], 0, 0, 0);
+                for (int n = 0; n < N32; n++) bf[ks][n] = *reinterpret_cast<const half8 *>(slot + rb[n][ks]);
             }
             if (cur.cs && id < TN) {
 #pragma unroll
                 for (int g = 0; g < 4; g++) cs_acc += csp[S][g][id];
             }
-            lds_fence_bar();
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            if (lane == 0) __hip_atomic_fetch_add(&s_empty[S], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            cq++;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int i = 0; i < M32; i++)
+#pragma unroll
+                    for (int n = 0; n < N32; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks][i], bf[ks][n], acc[i][n], 0, 0, 0);
             if (++st < cur.nst) return true;
             epilogue();
 #pragma unroll
