@@ -534,6 +534,19 @@ class KnnBench:
         self.out = (torch.empty((self.NQ, 128), dtype=torch.int64, device=dev),
                     torch.empty((self.NQ, 128), dtype=torch.float32, device=dev))
 
+    def wide_batch(self, dev, nq=4096, seed=4096):
+        """One batch of `nq` queries x 8 probes over the same store (cells shared by ~nq * 8 / 12288 queries each),
+        with its own output buffers."""
+        import torch
+        rng = np.random.default_rng(seed)
+        sizes = np.diff(self.cs)
+        q = rng.standard_normal((nq, self.D)).astype(np.float32)
+        p = np.stack([rng.choice(self.NCELLS, self.NPROBE, replace=False) for _ in range(nq)]).astype(np.int32)
+        return dict(q=torch.from_numpy(q).to(dev), p=torch.from_numpy(p).to(dev), qh=q, ph=p,
+                    pairs=int(sizes[p].sum()), bytes=int(sizes[np.unique(p)].sum()) * (self.D // 4 + 4),
+                    out=(torch.empty((nq, 128), dtype=torch.int64, device=dev),
+                         torch.empty((nq, 128), dtype=torch.float32, device=dev)))
+
     def search(self, i):
         bt = self.batches[i % len(self.batches)]
         return self.store.search_ivf(bt["q"], bt["p"], 128, out=self.out)
@@ -566,13 +579,17 @@ class KnnBench:
         byts = np.mean([self.batches[i % nb]["bytes"] for i in used])
         return ms, pairs, byts, dict(eager_ms=round(eager_ms, 5), graph_spread=spread)
 
-    def check(self, qis=(0, 100, 255)):
-        """Bit-exact top-128 for a few queries of batch 0 against the oracle over the same stored bytes."""
+    def check(self, qis=(0, 100, 255), bt=None):
+        """Bit-exact top-128 for a few queries of batch 0 (or of `bt`, a wide batch) against the oracle over the
+        same stored bytes."""
         import torch
         import oracle
-        idx, dist = self.search(0)
+        if bt is None:
+            idx, dist = self.search(0)
+            bt = self.batches[0]
+        else:
+            idx, dist = self.store.search_ivf(bt["q"], bt["p"], 128, out=bt["out"])
         idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
-        bt = self.batches[0]
         for qi in qis:
             cells = bt["ph"][qi]
             rows = np.concatenate([np.arange(self.cs[c], self.cs[c + 1]) for c in cells])
@@ -835,6 +852,23 @@ def main():
         if not args.no_cpu:
             knn["cpu_baseline"] = kb.cpu_baseline()
         extra["c5_knn"] = knn
+        log("[bench] C5 kNN store, one 4096-query batch")
+        wb = kb.wide_batch(dev)
+        if not kb.check((0, 1777, 4095), bt=wb):
+            log("[bench] PARITY FAILURE (4096-query batch): refusing to report")
+            sys.exit(3)
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup):
+                kb.store.search_ivf(wb["q"], wb["p"], 128, out=wb["out"])
+            torch.cuda.synchronize()
+            wsteps = max(1, min(args.steps, 5))
+            wms = time_graph_steps(lambda: kb.store.search_ivf(wb["q"], wb["p"], 128, out=wb["out"]), wsteps, stream)
+        wgbs = wb["bytes"] / wms / 1e6
+        extra["c5_knn_4096q"] = dict(ms_per_batch=round(wms, 5), queries=4096, pairs_per_batch=wb["pairs"],
+                                     g_keys_per_s=round(wb["pairs"] / wms / 1e6, 3),
+                                     distinct_cell_bytes=wb["bytes"], hbm_gbs=round(wgbs, 1),
+                                     hbm_frac=round(wgbs / PEAK["hbm_gbs"], 4), steps_per_graph=wsteps)
+        del wb
         log("[bench] C5 probe selection (12288 centroids, 256 queries x 8)")
         pb = ProbeBench(dev, [b["q"] for b in kb.batches])
         pok = pb.check()

@@ -34,8 +34,9 @@
 // 16 waves' 8th smallest (either has 128 keys at or below it).  Only keys with
 // at least 128 smaller keys are dropped, so the exact top-128 survives
 // whatever the order; the output position of each survivor is its rank.
-// Cells that other queries of the batch also probe are scanned first, so
-// their bytes are read while the other workgroups still find them in the MALL.
+// Cells that other queries of the same 256-query window (the workgroups that
+// run together) also probe are scanned first, so their bytes are read while
+// the other workgroups still find them in the MALL.
 #include <cstring>
 #include <type_traits>
 
@@ -154,6 +155,7 @@ __global__ __launch_bounds__(256) void k_synth_keys(uint64_t seed, int64_t row0,
 // ---------------------------------------------------------------- fused search
 
 constexpr int SW = 16;          // waves per search workgroup
+constexpr int SHARE_WIN = 256;  // queries whose cell sharing orders a query's cells (the CUs of the device)
 constexpr int STH = SW * 64;    // threads per search workgroup (one workgroup per query)
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -440,9 +442,14 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t q = blockIdx.x;
-    const int64_t total = MASKED ? 0 : (int64_t)nq * nprobe;
-    const int32_t pv0 = tid < total ? probes[tid] : -1;
-    const int32_t pv1 = tid + STH < total ? probes[tid + STH] : -1;
+    // Cell sharing is counted among the queries of q's window of SHARE_WIN
+    // (the workgroups that run at the same time, one per CU), so the count
+    // costs the same at any batch size.
+    const int64_t w0 = (q / SHARE_WIN) * SHARE_WIN, w1 = min((int64_t)nq, w0 + SHARE_WIN);
+    const int64_t pbase = w0 * nprobe;
+    const int64_t total = MASKED ? 0 : (w1 - w0) * nprobe;
+    const int32_t pv0 = tid < total ? probes[pbase + tid] : -1;
+    const int32_t pv1 = tid + STH < total ? probes[pbase + tid + STH] : -1;
 
     if (wave == 0) {
         const QInfo qi = quantize_query(queries + q * D, lane, s_Q);
@@ -472,10 +479,10 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         }
     }
     __syncthreads();
-    // How many (query, probe) pairs of the whole batch scan each probed cell
-    // (the first two probe ids per thread were loaded before the barrier).
+    // How many (query, probe) pairs of the window scan each probed cell (the
+    // first two probe ids per thread were loaded before the barrier).
     for (int64_t i = tid, it = 0; i < total; i += STH, it++) {
-        const int32_t v = it == 0 ? pv0 : it == 1 ? pv1 : probes[i];
+        const int32_t v = it == 0 ? pv0 : it == 1 ? pv1 : probes[pbase + i];
         for (int jj = 0; jj < nprobe; jj++)
             if (v == s_cell[jj]) atomicAdd(&s_share[jj], 1);
     }
