@@ -706,9 +706,9 @@ class ProbeBench:
 def device_ceilings(dev, stream):
     """Measured ceilings beside the published peaks every roofline is priced against: the matrix cores with only
     independent MFMA chains in flight (two waves per SIMD, 8 chains each; `mfma_f16` / `mfma_i8` in the 32 x 32
-    forms the kernels use, the 16 x 16 forms beside them), a streaming read of 1 GiB (one workgroup of 16
-    waves per CU, each reading its own slab with eight 16-byte loads per lane in flight, as the key scans read), and the
-    device's CU count and clocks (HIP device attributes)."""
+    forms the kernels use, the 16 x 16 forms beside them), a streaming read of 1 GiB (eight workgroups of 4 waves
+    per CU, each reading its own slab with sixteen nontemporal 16-byte loads per lane in flight: the fastest read
+    shape measured), and the device's CU count and clocks (HIP device attributes)."""
     import ctypes
     import torch
     from scratchtape_amd import _lib
@@ -726,7 +726,7 @@ def device_ceilings(dev, stream):
             ms = time_events(f, 5, stream)
             out[f"mfma_{name}_tflops_measured"] = round(blocks * waves * chains * iters * per / ms / 1e9, 1)
         buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-        g = lambda: _lib.call("st_peak_read", buf.data_ptr(), buf.numel() * 4, cus, sink.data_ptr(),
+        g = lambda: _lib.call("st_peak_read", buf.data_ptr(), buf.numel() * 4, 8 * cus, sink.data_ptr(),
                               stream.cuda_stream)
         g()
         ms = time_events(g, 10, stream)

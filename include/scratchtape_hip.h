@@ -306,8 +306,8 @@ st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *mem_clock_kh
 st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink, st_stream stream);
 
 /* Reads `bytes` (a multiple of 16, 16-byte aligned) of src once with `blocks`
- * workgroups of 1024 threads, each streaming its own contiguous slab; `sink` as
- * for st_peak_mfma. */
+ * workgroups of 256 threads, each streaming its own contiguous slab with
+ * nontemporal loads; `sink` as for st_peak_mfma. */
 st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks, float *sink, st_stream stream);
 
 /* ---- Misc ---------------------------------------------------------------- */

@@ -18,9 +18,11 @@
 // with every f32 operation separately rounded (contraction off), which the CPU
 // oracle reproduces bit for bit.  Ranking is by (dist, key index) ascending.
 //
-// Search design: one 1024-thread workgroup (16 wave64s) per query streams the
-// concatenation of its probed cells in 64-key chunks, each wave with three
-// chunks in flight.  Scoring runs on the matrix cores: the key codes are FP4
+// Search design: one 512-thread workgroup (8 wave64s) per query streams the
+// concatenation of its probed cells in 64-key chunks, each wave with five
+// chunks in flight (two waves per SIMD with up to 256 VGPRs each hold more
+// bytes in flight than four waves with 128, and the scoring of one chunk
+// hides behind the loads of the next four).  Scoring runs on the matrix cores: the key codes are FP4
 // e2m1 operands as stored (a 2-bit code in the low bits of a nibble is u / 2),
 // the query is four FP8 rows of balanced base-16 digits, and one scaled
 // FP8 x FP4 MFMA per 128 dims gives the exact integer dot of 16 keys; one
@@ -31,12 +33,13 @@
 // atomics, no workgroup barrier in the scan); when the list holds 192 a
 // wave-level bitonic sort keeps its 128 smallest, publishes its 8th smallest,
 // and the threshold drops to the smaller of its 128th and the largest of the
-// 16 waves' 8th smallest (either has 128 keys at or below it).  Only keys with
+// 8 waves' 16th smallest (either has 128 keys at or below it).  Only keys with
 // at least 128 smaller keys are dropped, so the exact top-128 survives
 // whatever the order; the output position of each survivor is its rank.
-// Cells that other queries of the same 256-query window (the workgroups that
-// run together) also probe are scanned first, so their bytes are read while
-// the other workgroups still find them in the MALL.
+// A query's cells are scanned in increasing id order.  (Scanning the cells
+// other queries of the batch also probe first, so that their second reads hit
+// the MALL, bought nothing: on this device a MALL-resident buffer reads no
+// faster than a stream from HBM.)
 #include <cstring>
 #include <type_traits>
 
@@ -154,9 +157,9 @@ __global__ __launch_bounds__(256) void k_synth_keys(uint64_t seed, int64_t row0,
 
 // ---------------------------------------------------------------- fused search
 
-constexpr int SW = 16;          // waves per search workgroup
-constexpr int SHARE_WIN = 256;  // queries whose cell sharing orders a query's cells (the CUs of the device)
+constexpr int SW = 8;           // waves per search workgroup
 constexpr int STH = SW * 64;    // threads per search workgroup (one workgroup per query)
+constexpr int NF = 5;           // chunks in flight per wave
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -319,15 +322,23 @@ struct Chunk {
     int32_t lo, hi, g;
 };
 
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// The codes are read with nontemporal (streaming) loads: a query reads each of
+// its keys once, and the device sustains a higher read rate for streaming
+// loads than for loads that allocate for reuse (about 6.8 against 6.0 TB/s).
+// The scales keep ordinary loads (256 B per chunk; streaming them measured
+// slower).
 template <bool SMALL>
 __device__ __forceinline__ void load_chunk(const uint8_t *codes, const float *scales, int64_t base, int64_t nrows,
                                            int row, int col, int lane, Chunk &ch) {
-    const uint4 *cb = reinterpret_cast<const uint4 *>(codes + base * (D / 4));
+    const v4u *cb = reinterpret_cast<const v4u *>(codes + base * (D / 4));
 #pragma unroll
     for (int G = 0; G < 4; G++) {
         int32_t kk = 16 * G + col;
         if (SMALL) kk = kk < nrows ? kk : 0;
-        ch.c[G] = cb[kk * 4 + row];
+        const v4u t = __builtin_nontemporal_load(cb + kk * 4 + row);
+        ch.c[G] = uint4{t.x, t.y, t.z, t.w};
     }
     ch.sc = scales[base + (SMALL ? (lane < nrows ? lane : 0) : lane)];
 }
@@ -378,7 +389,7 @@ __device__ __forceinline__ void score_chunk(const Chunk &ch, const v8i (&aq)[2],
     n12 = (int32_t)(z[0] + z[1]);
 }
 
-constexpr int E8 = KMAX / SW;  // each wave's published rank: SW * E8 = KMAX keys
+constexpr int E8 = (KMAX + SW - 1) / SW;  // each wave's published rank: SW * E8 >= KMAX keys
 
 typedef __attribute__((address_space(3))) uint64_t lds_u64;
 
@@ -435,21 +446,11 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     __shared__ int16_t s_Q[D];
     __shared__ float s_qs, s_qn;
     __shared__ int32_t s_sq, s_np, count, s_next;
-    __shared__ int32_t s_cell[PROBE_MAX], s_share[PROBE_MAX];
-    __shared__ int64_t s_c0[PROBE_MAX], s_c1[PROBE_MAX];
     __shared__ int64_t s_r0[PROBE_MAX], s_nrows;
     __shared__ int32_t s_len[PROBE_MAX], s_cpre[PROBE_MAX + 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t q = blockIdx.x;
-    // Cell sharing is counted among the queries of q's window of SHARE_WIN
-    // (the workgroups that run at the same time, one per CU), so the count
-    // costs the same at any batch size.
-    const int64_t w0 = (q / SHARE_WIN) * SHARE_WIN, w1 = min((int64_t)nq, w0 + SHARE_WIN);
-    const int64_t pbase = w0 * nprobe;
-    const int64_t total = MASKED ? 0 : (w1 - w0) * nprobe;
-    const int32_t pv0 = tid < total ? probes[pbase + tid] : -1;
-    const int32_t pv1 = tid + STH < total ? probes[pbase + tid + STH] : -1;
 
     if (wave == 0) {
         const QInfo qi = quantize_query(queries + q * D, lane, s_Q);
@@ -458,18 +459,61 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             s_qn = qi.qn;
             s_sq = qi.sq;
         }
-    } else if (wave == 1 && !MASKED) {
-        // The probed cells and their row ranges (all loads in flight together);
-        // an id outside [0, ncells) is recorded as -1 and skipped.
-        if (lane < nprobe) {
-            const int32_t c = probes[q * nprobe + lane];
-            const bool ok = c >= 0 && c < ncells;
-            s_cell[lane] = ok ? c : -1;
-            s_share[lane] = 0;
-            s_c0[lane] = ok ? cell_start[c] : 0;
-            s_c1[lane] = ok ? cell_start[c + 1] : 0;
+    } else if (wave == 1 && MASKED) {
+        if (lane == 0) {
+            // Segments [0, min(always, nkeys)) and [max(lo, always), min(hi, nkeys)).
+            const int64_t lo = lohi[2 * q], hi = lohi[2 * q + 1];
+            const int64_t a1 = always < nkeys ? always : nkeys;
+            const int64_t b0 = lo > always ? lo : always, b1 = hi < nkeys ? hi : nkeys;
+            int np = 0;
+            s_cpre[0] = 0;
+            if (a1 > 0) {
+                s_r0[np] = 0;
+                s_len[np] = (int32_t)a1;
+                s_cpre[np + 1] = (int32_t)((a1 + 63) / 64);
+                np++;
+            }
+            if (b1 > b0) {
+                s_r0[np] = b0;
+                s_len[np] = (int32_t)(b1 - b0);
+                s_cpre[np + 1] = s_cpre[np] + (int32_t)((b1 - b0 + 63) / 64);
+                np++;
+            }
+            s_np = np;
+            s_nrows = nkeys;
         }
+    } else if (wave == 1) {
+        // The probed cells in increasing id order (lane j loads probe j; all
+        // loads in flight together), a repeated id once, an id outside
+        // [0, ncells) skipped; s_cpre counts 64-key chunks.  Each lane finds its
+        // cell's place from the other lanes' ids (readlane), with no serial
+        // sort.
+        const int32_t c = lane < nprobe ? probes[q * nprobe + lane] : -1;
+        const bool ok = lane < nprobe && c >= 0 && c < ncells;
+        const int64_t r0 = ok ? cell_start[c] : 0, r1 = ok ? cell_start[c + 1] : 0;
         if (lane == 63) s_nrows = cell_start[ncells];
+        const int32_t key = ok ? c : INT32_MAX;
+        bool dup = false;
+        for (int i = 0; i < nprobe; i++) dup |= i < lane && __builtin_amdgcn_readlane(key, i) == key;
+        const bool keep = ok && !dup;
+        const int32_t nch = keep ? (int32_t)((r1 - r0 + 63) / 64) : 0;
+        int32_t pos = 0, cum = 0;
+        for (int i = 0; i < nprobe; i++) {
+            const int32_t ki = __builtin_amdgcn_readlane(key, i);
+            const bool kpi = __builtin_amdgcn_readlane((int32_t)keep, i) != 0;
+            pos += kpi && ki < key;
+            cum += kpi && ki <= key ? __builtin_amdgcn_readlane(nch, i) : 0;
+        }
+        if (keep) {
+            s_r0[pos] = r0;
+            s_len[pos] = (int32_t)(r1 - r0);
+            s_cpre[pos + 1] = cum;
+        }
+        const int np = __popcll(__ballot(keep));
+        if (lane == 0) {
+            s_cpre[0] = 0;
+            s_np = np;
+        }
     } else if (wave == 2) {
         if (lane < SW) s_e8[lane] = NONE;
         if (lane == 0) {
@@ -477,66 +521,6 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
             count = 0;
             s_next = 0;
         }
-    }
-    __syncthreads();
-    // How many (query, probe) pairs of the window scan each probed cell (the
-    // first two probe ids per thread were loaded before the barrier).
-    for (int64_t i = tid, it = 0; i < total; i += STH, it++) {
-        const int32_t v = it == 0 ? pv0 : it == 1 ? pv1 : probes[pbase + i];
-        for (int jj = 0; jj < nprobe; jj++)
-            if (v == s_cell[jj]) atomicAdd(&s_share[jj], 1);
-    }
-    __syncthreads();
-    if (MASKED && tid == 0) {
-        // Segments [0, min(always, nkeys)) and [max(lo, always), min(hi, nkeys)).
-        const int64_t lo = lohi[2 * q], hi = lohi[2 * q + 1];
-        const int64_t a1 = always < nkeys ? always : nkeys;
-        const int64_t b0 = lo > always ? lo : always, b1 = hi < nkeys ? hi : nkeys;
-        int np = 0;
-        s_cpre[0] = 0;
-        if (a1 > 0) {
-            s_r0[np] = 0;
-            s_len[np] = (int32_t)a1;
-            s_cpre[np + 1] = (int32_t)((a1 + 63) / 64);
-            np++;
-        }
-        if (b1 > b0) {
-            s_r0[np] = b0;
-            s_len[np] = (int32_t)(b1 - b0);
-            s_cpre[np + 1] = s_cpre[np] + (int32_t)((b1 - b0 + 63) / 64);
-            np++;
-        }
-        s_np = np;
-        s_nrows = nkeys;
-    } else if (!MASKED && tid == 0) {
-        // Cells scanned by several queries of the batch first (their bytes are
-        // then read while still in the MALL), a repeated cell once, invalid ids
-        // skipped; s_cpre counts 64-key chunks.
-        int order[PROBE_MAX];
-        for (int j = 0; j < nprobe; j++) {
-            int i = j;
-            while (i > 0 && (s_share[order[i - 1]] < s_share[j] ||
-                             (s_share[order[i - 1]] == s_share[j] && s_cell[order[i - 1]] > s_cell[j]))) {
-                order[i] = order[i - 1];
-                i--;
-            }
-            order[i] = j;
-        }
-        int np = 0;
-        int32_t prev = -1;
-        s_cpre[0] = 0;
-        for (int i = 0; i < nprobe; i++) {
-            const int j = order[i];
-            const int32_t c = s_cell[j];
-            if (c < 0 || c == prev) continue;
-            prev = c;
-            const int64_t len = s_c1[j] - s_c0[j];
-            s_r0[np] = s_c0[j];
-            s_len[np] = (int32_t)len;
-            s_cpre[np + 1] = s_cpre[np] + (int32_t)((len + 63) / 64);
-            np++;
-        }
-        s_np = np;
     }
     __syncthreads();
 
@@ -580,11 +564,11 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     };
 
     // Each wave keeps its own candidate list (no workgroup barrier in the scan,
-    // so the 16 waves drift apart and hide each other's memory latency).  Any
+    // so the waves drift apart and hide each other's memory latency).  Any
     // key above a threshold t with at least 128 scored keys at or below it can
     // be dropped.  Two such thresholds are kept: the wave's own 128th smallest
-    // key, and the largest of the waves' published E8-th smallest keys (16
-    // waves x 8 keys at or below it).  Their minimum over the workgroup lives
+    // key, and the largest of the waves' published E8-th smallest keys (SW
+    // waves x E8 keys at or below it).  Their minimum over the workgroup lives
     // in s_tau, which only decreases.
     // Each wave's list: wl[0, KMAX) holds its kept keys sorted ascending
     // (na of them, then NONE or larger keys already dropped), wl[KMAX, CAPW)
@@ -640,43 +624,39 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
         if (merge && nb > 64) wave_compact();  // at most 128 new keys
     };
 
-    // Three chunks per wave in flight: while one is scored the next two load.
+    // NF chunks per wave in flight: while one is scored the next NF - 1 load.
     // (Every step runs unconditionally: a chunk past the end has lo == hi and
     // scores nothing, and the loop body stays free of branches around loads.)
     // The empty asm with a memory clobber pins each fetch's loads above the
     // scoring that follows (the compiler would otherwise sink them to their
     // first use); nothing reads the loaded registers there, so no wait is added.
     auto scan = [&](auto small) {
-        Chunk x0, x1, x2;
-        // Phase A: each wave's first two chunks (2048 keys over the
-        // workgroup), every key kept; each wave sorts its 128 and publishes its E8-th
-        // smallest, and after one barrier every wave starts from the largest
-        // of those (about the 200th smallest of the 2048).
-        fetch(small, x0);
-        fetch(small, x1);
-        fetch(small, x2);
+        Chunk x[NF];
+        // Phase A: each wave's first two chunks (1024 keys over the
+        // workgroup), every key kept; each wave sorts its 128 and publishes
+        // its E8-th smallest, and after one barrier every wave starts from the
+        // largest of those.
+#pragma unroll
+        for (int i = 0; i < NF; i++) fetch(small, x[i]);
         asm volatile("" ::: "memory");
-        score(x0, false);
-        score(x1, false);
+        score(x[0], false);
+        score(x[1], false);
         wave_compact();
-        fetch(small, x0);
-        fetch(small, x1);
+        fetch(small, x[0]);
+        fetch(small, x[1]);
         asm volatile("" ::: "memory");
         __syncthreads();
         refresh();
-        // Phase B: the rest, three chunks per trip (x2, x0, x1 hold this
-        // wave's next chunks in increasing order: once x2's is past the end,
-        // so are the others).
-        while (x2.g < nchunks) {
-            score(x2);
-            fetch(small, x2);
-            asm volatile("" ::: "memory");
-            score(x0);
-            fetch(small, x0);
-            asm volatile("" ::: "memory");
-            score(x1);
-            fetch(small, x1);
-            asm volatile("" ::: "memory");
+        // Phase B: the rest, NF chunks per trip (x[2], ..., x[NF - 1], x[0],
+        // x[1] hold this wave's next chunks in increasing order: once x[2]'s
+        // is past the end, so are the others).
+        while (x[2].g < nchunks) {
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                score(x[(i + 2) % NF]);
+                fetch(small, x[(i + 2) % NF]);
+                asm volatile("" ::: "memory");
+            }
         }
     };
     if (nchunks > 0) {  // uniform over the workgroup
@@ -687,7 +667,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     }
     // Final: every wave sorts its list and keeps at most its best 128; the keys
     // at or below the final threshold (a superset of the query's top 128, at
-    // most 16 x 128) are gathered, and each one's rank among them (keys are
+    // most SW x 128) are gathered, and each one's rank among them (keys are
     // distinct: the index is part of the key) is its output position.
     wave_compact();
     __syncthreads();
