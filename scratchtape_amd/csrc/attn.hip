@@ -43,6 +43,7 @@
 // row 4g + e of the first tile (e < 4) or of the second (e >= 4), the order in
 // which the 16x16 accumulator layout hands them out; A and B agree on it.
 #include "common.h"
+#include "lanes.h"
 
 namespace {
 
@@ -145,10 +146,10 @@ __device__ __forceinline__ void stage(const float *x, int64_t ld, int n, _Float1
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     float p = v[e][k].x * w[e][k].x + v[e][k].y * w[e][k].y + v[e][k].z * w[e][k].z + v[e][k].w * w[e][k].w;
-                    p += __shfl_xor(p, 1, 64);
-                    p += __shfl_xor(p, 2, 64);
-                    p += __shfl_xor(p, 4, 64);
-                    p += __shfl_xor(p, 8, 64);
+                    p += st::xor_lane(p, 1, tid & 63);
+                    p += st::xor_lane(p, 2, tid & 63);
+                    p += st::xor_lane(p, 4, tid & 63);
+                    p += st::xor_lane(p, 8, tid & 63);
                     if ((i & 15) == 0) o[r0 + k] = p;
                 }
             }
@@ -248,8 +249,8 @@ __global__ __launch_bounds__(SplitF<NB>::NT) void k_attn_fwd(const float *__rest
                 for (int e = 0; e < 4; e++) ka[e] = kn[e];
             }
         }
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        m = fmaxf(m, st::xor_lane(m, 16, lane));
+        m = fmaxf(m, st::xor_lane(m, 32, lane));
         if (one) m = fmaxf(m, 0.f);
         float sum = 0.f;
 #pragma unroll
@@ -263,8 +264,8 @@ __global__ __launch_bounds__(SplitF<NB>::NT) void k_attn_fwd(const float *__rest
                 }
             }
         }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
+        sum += st::xor_lane(sum, 16, lane);
+        sum += st::xor_lane(sum, 32, lane);
         if (one) sum += exp2_(-m);
         const float inv = 1.f / sum;
         // O^T = V^T P^T over the same pairs, the next pair's V^T fragments read ahead.
@@ -411,8 +412,8 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
                        (_Float16)dv[3].x, (_Float16)dv[3].y, (_Float16)dv[3].z, (_Float16)dv[3].w};
 #pragma unroll
             for (int k = 0; k < 4; k++) dsum += dv[k].x * ov[k].x + dv[k].y * ov[k].y + dv[k].z * ov[k].z + dv[k].w * ov[k].w;
-            dsum += __shfl_xor(dsum, 16, 64);
-            dsum += __shfl_xor(dsum, 32, 64);
+            dsum += st::xor_lane(dsum, 16, lane);
+            dsum += st::xor_lane(dsum, 32, lane);
             L = lrow[q] * LOG2E;
         }
         // K (row-major and transposed) and V of every key.

@@ -117,6 +117,18 @@ __device__ __forceinline__ T *uni(T *v) {
     return reinterpret_cast<T *>(uni(reinterpret_cast<int64_t>(v)));
 }
 
+// Device memory reached through a global-address-space pointer.  The group's
+// pointers come from LDS, so the compiler cannot tell them from LDS addresses
+// and would emit flat loads and stores; a flat store also counts against the
+// LDS wait counter, so the next wait for an LDS read (every consumer stage
+// has one) would wait until the epilogue's stores reached memory.
+template <class T>
+using gptr = T __attribute__((address_space(1))) *;
+template <class T>
+__device__ __forceinline__ gptr<T> glb(T *p) {
+    return (gptr<T>)p;
+}
+
 // First unit of XCD x's block of GEMM p's units: x U / 8 of U.
 __device__ __forceinline__ int block_start(int x, int units) { return (int)((int64_t)x * units / XCDS); }
 
@@ -357,9 +369,9 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 
         if (do_cs && tid < TN) {
             if (gsplits > 1)
-                g.cs[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
+                glb(g.cs)[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + tid] = cs_acc;
             else
-                g.cs[cur.zb * g.cs_stride + cur.col0 + tid] += cs_acc;
+                glb(g.cs)[cur.zb * g.cs_stride + cur.col0 + tid] += cs_acc;
         }
         // Epilogue through LDS: the slot of the unit's last stage is free
         // until the next unit's first barrier (the next stage issued into it
@@ -379,8 +391,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
             float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
             const int64_t o0 = uni(split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner));
             const int64_t ld = uni((int64_t)(split ? g.n : g.ldo));
-            float *const obase = uni(split ? P : g.out + o0);
-            const float *const bias = uni(g.bias), *const mask = uni(g.mask), *const res = uni(g.res);
+            const gptr<float> obase = glb(uni(split ? P : g.out + o0));
+            const gptr<const float> bias = glb(uni(g.bias)), mask = glb(uni(g.mask)), res = glb(uni(g.res));
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 if constexpr (F16) {
@@ -407,7 +419,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                     const int64_t idx = (int64_t)grow * ld + gcol;
                     if (!split) {
                         if (bias) {
-                            const float *bp = bias + cur.zb * g.bias_stride + gcol;
+                            const gptr<const float> bp = bias + cur.zb * g.bias_stride + gcol;
 #pragma unroll
                             for (int x = 0; x < 4; x++) v[x] += bp[x];
                         }
@@ -416,15 +428,15 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                             for (int x = 0; x < 4; x++) v[x] = v[x] < 0.f ? 0.f : v[x];
                         }
                         if (mask) {
-                            const f32x4 mk = *reinterpret_cast<const f32x4 *>(mask + o0 + idx);
+                            const f32x4 mk = *(gptr<const f32x4>)(mask + o0 + idx);
 #pragma unroll
                             for (int x = 0; x < 4; x++)
                                 if (mk[x] <= 0.f) v[x] = 0.f;
                         }
-                        if (res) v += *reinterpret_cast<const f32x4 *>(res + o0 + idx);
-                        if (gflags & F_ACC) v += *reinterpret_cast<const f32x4 *>(obase + idx);
+                        if (res) v += *(gptr<const f32x4>)(res + o0 + idx);
+                        if (gflags & F_ACC) v += *(gptr<const f32x4>)(obase + idx);
                     }
-                    *reinterpret_cast<f32x4 *>(obase + idx) = v;
+                    *(gptr<f32x4>)(obase + idx) = v;
                 }
             }
         }
@@ -793,8 +805,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
         const int64_t o0 = uni(split ? 0 : zoff(cur.zb, g.o_group, g.o_stride, g.o_inner));
         const int64_t ld = uni((int64_t)(split ? g.n : g.ldo));
-        float *const obase = uni(split ? P : g.out + o0);
-        const float *const bias = uni(g.bias), *const mask = uni(g.mask), *const res = uni(g.res);
+        const gptr<float> obase = glb(uni(split ? P : g.out + o0));
+        const gptr<const float> bias = glb(uni(g.bias)), mask = glb(uni(g.mask)), res = glb(uni(g.res));
         const int64_t lane_off = (int64_t)(4 * (lane >> 5)) * ld + (lane & 31);
 #pragma unroll
         for (int n = 0; n < N32; n++) {
@@ -846,9 +858,9 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         }
         if (cur.cs && id < TN) {
             if (split)
-                g.cs[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + id] = cs_acc;
+                glb(g.cs)[(cur.zb * gsplits + cur.slice) * (int64_t)g.n + cur.col0 + id] = cs_acc;
             else
-                g.cs[cur.zb * g.cs_stride + cur.col0 + id] += cs_acc;
+                glb(g.cs)[cur.zb * g.cs_stride + cur.col0 + id] += cs_acc;
         }
     };
 
@@ -980,10 +992,10 @@ __global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
     if (local < 0) return;
     if (local < s.batch * s.mn4) {
         const int64_t b = local / s.mn4, i = local % s.mn4;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(s.part) + b * s.splits * s.mn4 + i;
+        const gptr<const f32x4> src = (gptr<const f32x4>)s.part + b * s.splits * s.mn4 + i;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         for (int sl = 0; sl < s.splits; sl++) v += src[sl * s.mn4];
-        f32x4 *o = reinterpret_cast<f32x4 *>(s.out + b * s.o_stride) + i;
+        const gptr<f32x4> o = (gptr<f32x4>)(s.out + b * s.o_stride) + i;
         if (s.accumulate) v += *o;
         *o = v;
     } else if (s.cs_part) {
@@ -991,8 +1003,8 @@ __global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
         if (c < s.batch * s.n) {
             const int64_t b = c / s.n, jn = c % s.n;
             float v = 0.f;
-            for (int sl = 0; sl < s.splits; sl++) v += s.cs_part[(b * s.splits + sl) * s.n + jn];
-            s.cs_dst[b * s.cs_stride + jn] += v;
+            for (int sl = 0; sl < s.splits; sl++) v += glb(s.cs_part)[(b * s.splits + sl) * s.n + jn];
+            glb(s.cs_dst)[b * s.cs_stride + jn] += v;
         }
     }
 }

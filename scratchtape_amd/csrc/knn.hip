@@ -44,6 +44,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "lanes.h"
 
 #pragma clang fp contract(off)
 
@@ -162,15 +163,13 @@ constexpr int STH = SW * 64;    // threads per search workgroup (one workgroup p
 constexpr int NF = 5;           // chunks in flight per wave
 
 __device__ __forceinline__ float wave_max(float v) {
+    const int lane = st::lane_id();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, st::xor_lane(v, o, lane));
     return v;
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
-    return ((uint64_t)hi << 32) | lo;
-}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m, int lane) { return st::xor_lane(v, m, lane); }
 
 // Bitonic networks over the 64 R keys of one wave held in registers: element
 // e = 64 r + lane sits in lane `lane`, register r.  Exchanges across lanes
@@ -194,7 +193,7 @@ __device__ __forceinline__ void bitonic_pass(uint64_t (&x)[R], int lane) {
     } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint64_t y = shfl_xor_u64(x[r], J);
+            const uint64_t y = shfl_xor_u64(x[r], J, lane);
             const bool asc = ((r * 64 + lane) & K) == 0;
             const bool take_min = ((lane & J) == 0) == asc;
             x[r] = (take_min == (x[r] < y)) ? x[r] : y;
@@ -217,10 +216,10 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&x)[R], int lane) {
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    const int lane = st::lane_id();
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
-        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        const uint64_t w = st::xor_lane(v, o, lane);
         v = w > v ? w : v;
     }
     return v;
@@ -253,8 +252,8 @@ __device__ __forceinline__ QInfo quantize_query(const float *qrow, int lane, int
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        sq += __shfl_xor(sq, o, 64);
-        sq2 += __shfl_xor(sq2, o, 64);
+        sq += st::xor_lane(sq, o, lane);
+        sq2 += st::xor_lane(sq2, o, lane);
     }
     return QInfo{qs, (float)sq2 * (qs * qs), sq};
 }
@@ -413,7 +412,7 @@ __device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, in
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const uint64_t a = r * 64 + lane < na ? wl[r * 64 + lane] : NONE;
-        const uint64_t b = shfl_xor_u64(nk[1 - r], 63);  // new key 127 - (64 r + lane)
+        const uint64_t b = shfl_xor_u64(nk[1 - r], 63, lane);  // new key 127 - (64 r + lane)
         kp[r] = a < b ? a : b;
     }
     bitonic_stage<2, 128, 64>(kp, lane);

@@ -45,6 +45,7 @@
 // dd never leaves the chip; per query only the candidates (about nprobe per
 // slice) are written and read back.
 #include "common.h"
+#include "lanes.h"
 
 #pragma clang fp contract(off)
 
@@ -65,8 +66,9 @@ typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float wave_max(float v) {
+    const int lane = st::lane_id();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, st::xor_lane(v, o, lane));
     return v;
 }
 
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) void k_probe_prep(const float *__restrict__ x,
     if (norm) {
         double t2 = (double)s2;  // partial sums are integers below 2^53: exact in any order
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) t2 += __shfl_xor(t2, o, 64);
+        for (int o = 32; o > 0; o >>= 1) t2 += st::xor_lane(t2, o, lane);
         if (lane == 0) norm[r] = ldexp(t2, 2 * (e - 14));
     }
     if (lane == 0) ex[r] = e - 14;
@@ -135,17 +137,14 @@ __device__ __forceinline__ bool lt(uint64_t ka, int32_t ia, uint64_t kb, int32_t
     return ka < kb || (ka == kb && ia < ib);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
-    return ((uint64_t)hi << 32) | lo;
-}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) { return st::xor_lane(v, m, st::lane_id()); }
 
 // Wave-wide minimum of (key, id); every lane receives it.
 __device__ __forceinline__ void wave_min(uint64_t &k, int32_t &i) {
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         const uint64_t ko = shfl_xor_u64(k, o);
-        const int32_t io = __shfl_xor(i, o, 64);
+        const int32_t io = st::xor_lane(i, o, st::lane_id());
         if (lt(ko, io, k, i)) {
             k = ko;
             i = io;
@@ -159,7 +158,7 @@ __device__ __forceinline__ uint32_t wave_sort_u32(uint32_t x, int lane) {
     for (int k = 2; k <= 64; k <<= 1) {
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint32_t y = __shfl_xor(x, j, 64);
+            const uint32_t y = st::xor_lane(x, j, lane);
             const bool take_min = ((lane & j) == 0) == ((lane & k) == 0);
             x = take_min ? min(x, y) : max(x, y);
         }
@@ -174,7 +173,7 @@ __device__ __forceinline__ void wave_sort_pair(uint64_t &k, int32_t &i, int lane
 #pragma unroll
         for (int j = kk >> 1; j > 0; j >>= 1) {
             const uint64_t ko = shfl_xor_u64(k, j);
-            const int32_t io = __shfl_xor(i, j, 64);
+            const int32_t io = st::xor_lane(i, j, lane);
             const bool take_min = ((lane & j) == 0) == ((lane & kk) == 0);
             if (take_min == lt(ko, io, k, i)) {
                 k = ko;
@@ -288,7 +287,7 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
             for (int v = 0; v < 8; v++) {
                 const int32_t lo8 = acc[v], hi8 = acc[8 + v];
                 const int32_t own = lo8 ^ ((lo8 ^ hi8) & om);
-                const int32_t got = __shfl_xor(hi8 ^ ((lo8 ^ hi8) & om), 1, 64);
+                const int32_t got = st::xor_lane(hi8 ^ ((lo8 ^ hi8) & om), 1, lane);
                 pch[v] = own ^ ((own ^ got) & om);
                 pcl[v] = got ^ ((own ^ got) & om);
             }
@@ -324,7 +323,7 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
         for (int kk = 2; kk <= 16; kk <<= 1) {
 #pragma unroll
             for (int j = kk >> 1; j > 0; j >>= 1) {
-                const uint32_t y = __shfl_xor(x, 2 * j, 64);
+                const uint32_t y = st::xor_lane(x, 2 * j, lane);
                 const bool take_min = ((c16 & j) == 0) == ((c16 & kk) == 0);
                 x = take_min ? min(x, y) : max(x, y);
             }
@@ -409,7 +408,7 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
 #pragma unroll
                 for (int d = 2; d < 32; d <<= 1) {  // minimum over the group (lane bits 1..4)
                     const uint64_t ko = shfl_xor_u64(bk, d);
-                    const int32_t io = __shfl_xor(bi, d, 64);
+                    const int32_t io = st::xor_lane(bi, d, lane);
                     if (lt(ko, io, bk, bi)) {
                         bk = ko;
                         bi = io;

@@ -1,0 +1,74 @@
+// Cross-lane exchanges within a wave64 that stay in the VALU.
+//
+// __shfl_xor compiles to ds_bpermute_b32, which goes through the LDS unit:
+// roughly a hundred cycles per exchange, and a butterfly or bitonic network
+// chains many of them.  xor_lane(v, j, lane) returns lane (lane ^ j)'s v for
+// j a power of two below 64 with
+//   j = 1, 2   a DPP quad permutation ([1,0,3,2], [2,3,0,1]);
+//   j = 4      DPP row_shl:4 (lane i reads i + 4) or row_shr:4 (i - 4) within
+//              the 16-lane row, picked by lane bit 2 (the lanes a shift leaves
+//              without a source are never picked);
+//   j = 8      DPP row_ror:8 (rotation by 8 within the row);
+//   j = 16, 32 v_permlane16_swap / v_permlane32_swap of v with itself: the
+//              swap returns (v with the odd rows / upper half replaced,
+//              v with the even rows / lower half replaced), and a lane takes
+//              the one holding its partner's value.
+// Each of the six was checked on the device against lane ^ j.  Inside an
+// unrolled loop j is a constant and the switch folds away; any other j falls
+// back to __shfl_xor.  Every lane of the wave must be active (as for a DPP
+// butterfly in general): callers use these in wave-uniform code only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace st {
+
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int j, int lane) {
+    switch (j) {
+        case 1:
+            return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+        case 2:
+            return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+        case 4: {
+            const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);
+            const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);
+            return (lane & 4) ? dn : up;
+        }
+        case 8:
+            return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+        case 16: {
+            const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            return (lane & 16) ? r[0] : r[1];
+        }
+        case 32: {
+            const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            return (lane & 32) ? r[0] : r[1];
+        }
+        default:
+            return (uint32_t)__shfl_xor((int)v, j, 64);
+    }
+}
+
+__device__ __forceinline__ int32_t xor_lane(int32_t v, int j, int lane) {
+    return (int32_t)xor_lane((uint32_t)v, j, lane);
+}
+
+__device__ __forceinline__ float xor_lane(float v, int j, int lane) {
+    return __builtin_bit_cast(float, xor_lane(__builtin_bit_cast(uint32_t, v), j, lane));
+}
+
+__device__ __forceinline__ uint64_t xor_lane(uint64_t v, int j, int lane) {
+    const uint32_t lo = xor_lane((uint32_t)v, j, lane), hi = xor_lane((uint32_t)(v >> 32), j, lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ double xor_lane(double v, int j, int lane) {
+    return __builtin_bit_cast(double, xor_lane(__builtin_bit_cast(uint64_t, v), j, lane));
+}
+
+// This lane's index in its wave64.
+__device__ __forceinline__ int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+}  // namespace st

@@ -20,20 +20,23 @@
 // per column, combined in a fixed order), then the chunks summed in order.  Contraction is off so that
 // scale*x - m rounds the product first, as the reference's CPU tape does.
 #include "common.h"
+#include "lanes.h"
 
 #pragma clang fp contract(off)
 
 namespace {
 
 __device__ __forceinline__ float wave_max(float v) {
+    const int lane = st::lane_id();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, st::xor_lane(v, o, lane));
     return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
+    const int lane = st::lane_id();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int o = 32; o > 0; o >>= 1) v += st::xor_lane(v, o, lane);
     return v;
 }
 
