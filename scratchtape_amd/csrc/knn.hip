@@ -423,7 +423,7 @@ __device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, in
     __builtin_amdgcn_wave_barrier();
     Kept k;
     k.na = __popcll(__ballot(kp[0] != NONE)) + __popcll(__ballot(kp[1] != NONE));
-    k.tau = ((uint64_t)__shfl((uint32_t)(kp[1] >> 32), 63, 64) << 32) | __shfl((uint32_t)kp[1], 63, 64);
+    k.tau = ((uint64_t)st::lane_value((uint32_t)(kp[1] >> 32), 63) << 32) | st::lane_value((uint32_t)kp[1], 63);
     return k;
 }
 

@@ -328,7 +328,11 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
                 x = take_min ? min(x, y) : max(x, y);
             }
         }
-        tau[u] = __shfl(x, 32 * h + 2 * (nprobe - 1) + odd, 64);
+        // Lane 32 h + 2 (nprobe - 1) + odd's x: four uniform reads, one picked per lane.
+        const int b = 2 * (nprobe - 1);
+        const uint32_t t0 = st::lane_value(x, b), t1 = st::lane_value(x, b + 1), t2 = st::lane_value(x, b + 32),
+                       t3 = st::lane_value(x, b + 33);
+        tau[u] = h ? (odd ? t3 : t2) : (odd ? t1 : t0);
     }
 
     // Candidates: the keys at or below their query's threshold, written at the
@@ -346,13 +350,24 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
             pm |= (uint32_t)(q < nq && kk != KNONE && (uint32_t)(kk >> 32) <= tau[u]) << k;
         }
         const int n = __popc(pm);
+        // Inclusive sum over the group's c16 = 0 .. 15 (lanes 32 h + 2 c16 +
+        // odd): DPP row shifts by 2, 4, 8 lanes scan the 8 positions of each
+        // 16-lane row, then the second row of each half adds the first row's
+        // total of its parity.
         int incl = n;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            const int y = __shfl_up(incl, 2 * d, 64);
-            if (c16 >= d) incl += y;
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);
+        {
+            const int r0 = st::lane_value(incl, 14), r1 = st::lane_value(incl, 15), r2 = st::lane_value(incl, 46),
+                      r3 = st::lane_value(incl, 47);
+            if (lane & 16) incl += h ? (odd ? r3 : r2) : (odd ? r1 : r0);
         }
-        cnt[u] = __shfl(incl, 32 * h + 30 + odd, 64);
+        {
+            const int c0 = st::lane_value(incl, 30), c1 = st::lane_value(incl, 31), c2 = st::lane_value(incl, 62),
+                      c3 = st::lane_value(incl, 63);
+            cnt[u] = h ? (odd ? c3 : c2) : (odd ? c1 : c0);
+        }
         int pos = incl - n;
         uint64_t *sk = ck + (int64_t)q * S * CAPQ + sl;
         int32_t *si = ci + (int64_t)q * S * CAPQ + sl;
@@ -514,18 +529,13 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
         uint32_t m = 0xffffffffu;
 #pragma unroll
         for (int e = 0; e < MREG; e++) m = min(m, (uint32_t)(kk[e] >> 32));
-        const uint32_t tau = __shfl(wave_sort_u32(m, lane), nprobe - 1, 64);
+        const uint32_t tau = st::lane_value(wave_sort_u32(m, lane), nprobe - 1);
         uint32_t pm = 0;
 #pragma unroll
         for (int e = 0; e < MREG; e++) pm |= (uint32_t)(kk[e] != KNONE && (uint32_t)(kk[e] >> 32) <= tau) << e;
         const int mine = __popc(pm);
-        int incl = mine;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
-        const int total = __shfl(incl, 63, 64);
+        const int incl = st::wave_incl_scan(mine);
+        const int total = st::lane_value(incl, 63);
         if (total <= 64) {
             int pos = incl - mine;
 #pragma unroll
@@ -568,20 +578,15 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
         const int32_t c = qc[sl];
         for (int e = 0; e < slot_size(c); e++) m = min(m, (uint32_t)(qk[(int64_t)slot_entry(c, e) * S + sl] >> 32));
     }
-    const uint32_t tau = __shfl(wave_sort_u32(m, lane), nprobe - 1, 64);
+    const uint32_t tau = st::lane_value(wave_sort_u32(m, lane), nprobe - 1);
     int mine = 0;
     for (int32_t sl = lane; sl < S; sl += 64) {
         const int32_t c = qc[sl];
         for (int e = 0; e < slot_size(c); e++)
             mine += (uint32_t)(qk[(int64_t)slot_entry(c, e) * S + sl] >> 32) <= tau;
     }
-    int incl = mine;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    const int total = __shfl(incl, 63, 64);
+    const int incl = st::wave_incl_scan(mine);
+    const int total = st::lane_value(incl, 63);
     if (total <= 64) {
         int pos = incl - mine;
         for (int32_t sl = lane; sl < S; sl += 64) {

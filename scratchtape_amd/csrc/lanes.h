@@ -9,11 +9,13 @@
 //              the 16-lane row, picked by lane bit 2 (the lanes a shift leaves
 //              without a source are never picked);
 //   j = 8      DPP row_ror:8 (rotation by 8 within the row);
+//   j = 15     DPP row_mirror (lane i of a row reads lane 15 - i); 63 is
+//              15, then 16, then 32;
 //   j = 16, 32 v_permlane16_swap / v_permlane32_swap of v with itself: the
 //              swap returns (v with the odd rows / upper half replaced,
 //              v with the even rows / lower half replaced), and a lane takes
 //              the one holding its partner's value.
-// Each of the six was checked on the device against lane ^ j.  Inside an
+// Each of these was checked on the device against lane ^ j.  Inside an
 // unrolled loop j is a constant and the switch folds away; any other j falls
 // back to __shfl_xor.  Every lane of the wave must be active (as for a DPP
 // butterfly in general): callers use these in wave-uniform code only.
@@ -38,6 +40,15 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int j, int lane) {
         }
         case 8:
             return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+        case 15:
+            return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+        case 63: {
+            const uint32_t m = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+            const auto r = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+            const uint32_t t = (lane & 16) ? r[0] : r[1];
+            const auto q = __builtin_amdgcn_permlane32_swap(t, t, false, false);
+            return (lane & 32) ? q[0] : q[1];
+        }
         case 16: {
             const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
             return (lane & 16) ? r[0] : r[1];
@@ -67,6 +78,24 @@ __device__ __forceinline__ uint64_t xor_lane(uint64_t v, int j, int lane) {
 __device__ __forceinline__ double xor_lane(double v, int j, int lane) {
     return __builtin_bit_cast(double, xor_lane(__builtin_bit_cast(uint64_t, v), j, lane));
 }
+
+// Inclusive prefix sum over the wave's 64 lanes: DPP row_shr 1, 2, 4, 8
+// within each row of 16 (a shift past the row's start reads 0), then
+// row_bcast:15 adds each even row's last lane to the row after it (rows 1, 3)
+// and row_bcast:31 adds lane 31 to rows 2 and 3.  Checked on the device.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+    return x;
+}
+
+// A wave-uniform lane's value (index known to be the same in every lane).
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, int src) { return (uint32_t)__builtin_amdgcn_readlane((int)v, src); }
+__device__ __forceinline__ int32_t lane_value(int32_t v, int src) { return __builtin_amdgcn_readlane(v, src); }
 
 // This lane's index in its wave64.
 __device__ __forceinline__ int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
