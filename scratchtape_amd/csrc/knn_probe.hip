@@ -24,11 +24,12 @@
 // lane l holding vector (l % 32) / 2, digit l % 2, dims 32 s + 16 (l / 32) ..
 // + 15, so an operand is one ds_read_b128 per k-step.
 //
-// Three launches per chunk of queries:
-//   k_probe_prep  the queries into digit tiles (as the centroids are, once per
-//                 index) and exponents;
+// k_probe_prep turns the centroids into digit tiles, exponents and norms once
+// per index.  Two launches per chunk of queries:
 //   k_probe_part  grid = centroid slices (up to 12 tiles) x groups of 64
-//                 queries.  The workgroup stages its slice in LDS and each wave
+//                 queries.  The workgroup turns its 64 queries into digit
+//                 tiles in LDS (as k_probe_prep would), stages its slice in
+//                 LDS, and each wave
 //                 scores its 16 queries against it, keeping the 12 x 4
 //                 order-preserving dd keys of its lane in registers.  A
 //                 per-query threshold -- the nprobe-th smallest of the 16
@@ -195,8 +196,7 @@ constexpr int32_t INONE = 0x7fffffff;
 // group) = (idx / gy, idx % gy) with idx dealt so that the gy workgroups of a
 // slice are consecutive on one XCD (workgroup ids go round robin over the 8
 // XCDs), which then reads the slice's digits from HBM once.
-__global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict__ qdig, const int32_t *__restrict__ qex,
-                                                    int32_t nq,
+__global__ __launch_bounds__(PART_T) void k_probe_part(const float *__restrict__ queries, int32_t nq,
                                                     const int8_t *__restrict__ cdig, const int32_t *__restrict__ cexp,
                                                     const double *__restrict__ cnorm, int32_t nlist, int32_t S,
                                                     int32_t gy, int32_t nprobe, uint64_t *__restrict__ ck,
@@ -205,6 +205,8 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
     __shared__ double s_cn[TPS * TILE];
     __shared__ int32_t s_ce[TPS * TILE];
     __shared__ uint32_t s_x[2][4][64][4];  // per (half, query tile, lane, u): minima, then counts
+    __shared__ v4i s_q[4 * TILE_BYTES / 16];  // the workgroup's 64 queries as 4 digit tiles
+    __shared__ int32_t s_qe[QG];              // and their exponents
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int qt = w & 3, half = w >> 2;  // query tile; tiles [half HT, half HT + HT) of the slice
     const int64_t nb = (int64_t)S * gy, b = blockIdx.x;
@@ -227,18 +229,52 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
         }
     }
 
-    // This wave's 16 queries (digit tile qg * 4 + qt of the prepared queries):
-    // lane l holds query (l % 32) / 2, digit l % 2, dims 32 s + 16 (l / 32) ..
+    // The workgroup's 64 queries into digit tiles in LDS (k_probe_prep's
+    // arithmetic and layout, wave w taking queries 8 w .. 8 w + 7, all eight
+    // rows' loads in flight together; a query past nq is a zero row).  Every
+    // slice's workgroup redoes this for its query group: 64 KB of f32 reads,
+    // in place of a separate launch.
+    {
+        float4 f[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int32_t q = qg * QG + w * 8 + t;
+            f[t] = q < nq ? reinterpret_cast<const float4 *>(queries + (int64_t)q * D)[lane]
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const int s_ = lane >> 3, hh = (lane & 7) >> 2, b0 = 4 * (lane & 3);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int v = w * 8 + t;
+            const float vv[4] = {f[t].x, f[t].y, f[t].z, f[t].w};
+            const float mx = wave_max(fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3]))));
+            int e = 14;  // scale 2^0 for a zero vector
+            if (mx > 0.f) frexpf(mx, &e);
+            uint32_t hi = 0, lo = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                int32_t xh, xl, X;
+                digits_of(vv[k], e, xh, xl, X);
+                lo |= (uint32_t)(xl & 255) << (8 * k);
+                hi |= (uint32_t)(xh & 255) << (8 * k);
+            }
+            char *blk = reinterpret_cast<char *>(s_q) + (v / TILE) * TILE_BYTES + s_ * 1024 + b0;
+            *reinterpret_cast<uint32_t *>(blk + (32 * hh + 2 * (v % TILE)) * 16) = hi;
+            *reinterpret_cast<uint32_t *>(blk + (32 * hh + 2 * (v % TILE) + 1) * 16) = lo;
+            if (lane == 0) s_qe[v] = e - 14;
+        }
+    }
+    __syncthreads();
+
+    // This wave's 16 queries (digit tile qt of the workgroup's): lane l holds
+    // query (l % 32) / 2, digit l % 2, dims 32 s + 16 (l / 32) ..
     const int h = lane >> 5, odd = lane & 1;
     const int q16 = (lane & 31) >> 1;
     const int32_t qbase = qg * QG + qt * 16;
     const bool wact = qbase < nq;
     v4i a[8];
 #pragma unroll
-    for (int s = 0; s < 8; s++)
-        a[s] = wact ? *reinterpret_cast<const v4i *>(qdig + (int64_t)(qbase / TILE) * TILE_BYTES + s * 1024 + lane * 16)
-                    : v4i{0, 0, 0, 0};
-    __syncthreads();
+    for (int s = 0; s < 8; s++) a[s] = wact ? s_q[qt * (TILE_BYTES / 16) + s * 64 + lane] : v4i{0, 0, 0, 0};
 
     // Output layout of the 32 x 32 MFMA: lane l holds column l % 32 (centroid
     // c16 = (l % 32) / 2, digit l % 2) and rows 8 j + 4 h + i (i < 4, j < 4):
@@ -251,31 +287,33 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         qu[u] = 4 * (2 * odd + u / 2) + 2 * h + (u & 1);
-        qeu[u] = qbase + qu[u] < nq ? qex[qbase + qu[u]] : 0;
+        qeu[u] = qbase + qu[u] < nq ? s_qe[qt * 16 + qu[u]] : 0;
     }
     // Every tile slot is scored (branch-free): a slot past the slice's tiles
     // reads stale LDS, and its centroid ids are >= nlist, so its keys are none.
     uint64_t key[HT][4];
     uint32_t mn[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    // The MFMAs of TG tiles at a time, k-step by k-step: TG independent
+    // accumulator chains interleaved keep the matrix core busy (each MFMA's
+    // input is TG instructions old); the group's keys are formed afterwards.
+    constexpr int TG = 3;
+    static_assert(HT % TG == 0, "tile groups");
 #pragma unroll
-    for (int k0 = 0; k0 < HT; k0++) {
-        const int k = half * HT + k0;
-        {
-            // Two accumulator chains (k-steps 0..3 and 4..7) halve the MFMA
-            // dependency chain; their sum is exact.
-            v16i acc, acc2;
+    for (int g0 = 0; g0 < HT; g0 += TG) {
+        v16i acc[TG];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                acc[i] = 0;
-                acc2[i] = 0;
-            }
+        for (int t = 0; t < TG; t++)
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], s_b[k * 512 + s * 64 + lane], acc, 0, 0, 0);
-                acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s + 4], s_b[k * 512 + (s + 4) * 64 + lane], acc2, 0, 0, 0);
-            }
+            for (int i = 0; i < 16; i++) acc[t][i] = 0;
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] += acc2[i];
+        for (int s = 0; s < 8; s++)
+#pragma unroll
+            for (int t = 0; t < TG; t++)
+                acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s], s_b[(half * HT + g0 + t) * 512 + s * 64 + lane],
+                                                              acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < TG; t++) {
+            const int k0 = g0 + t, k = half * HT + k0;
             // The even lane holds the products with the centroid's high digit,
             // the odd lane those with its low digit; each sends the other the
             // eight it needs.
@@ -285,7 +323,7 @@ __global__ __launch_bounds__(PART_T) void k_probe_part(const int8_t *__restrict_
             int32_t pch[8], pcl[8];
 #pragma unroll
             for (int v = 0; v < 8; v++) {
-                const int32_t lo8 = acc[v], hi8 = acc[8 + v];
+                const int32_t lo8 = acc[t][v], hi8 = acc[t][8 + v];
                 const int32_t own = lo8 ^ ((lo8 ^ hi8) & om);
                 const int32_t got = st::xor_lane(hi8 ^ ((lo8 ^ hi8) & om), 1, lane);
                 pch[v] = own ^ ((own ^ got) & om);
@@ -469,7 +507,8 @@ __device__ __forceinline__ int slot_size(int32_t c) { return (c & 0xffff) + ((c 
 
 constexpr int MREG = 24;  // candidates per lane held in registers by the merge
 
-// Four queries per workgroup, one wave each: probes[q][0, nprobe) by (key, id)
+// One wave per query (a workgroup of one wave, so the queries spread over
+// every CU): probes[q][0, nprobe) by (key, id)
 // ascending over the candidates of its S slots (lane l takes slots l, l + 64,
 // ..).  A threshold on the high 32 bits of the keys is the nprobe-th smallest
 // of the 64 lanes' minima, so at least nprobe candidates lie at or below it
@@ -483,7 +522,7 @@ __global__ __launch_bounds__(256) void k_probe_merge(const uint64_t *__restrict_
     __shared__ uint64_t s_k[4][64];
     __shared__ int32_t s_i[4][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t q = (int64_t)blockIdx.x * 4 + w;
+    const int64_t q = (int64_t)blockIdx.x * (blockDim.x >> 6) + w;
     if (q >= nqc) return;
     const uint64_t *qk = ck + q * S * CAPQ;
     const int32_t *qi = ci + q * S * CAPQ;
@@ -679,30 +718,25 @@ extern "C" st_status st_knn_probe(const int8_t *digits, const int32_t *cexp, con
 
     // Queries in chunks (multiples of 64) whose candidate slots fit CAND_BUDGET.
     const int64_t ntiles = cdiv(nlist, TILE), S = cdiv(ntiles, TPS);
-    const int64_t per_q = S * CAPQ * (int64_t)(sizeof(uint64_t) + sizeof(int32_t)) + S * (int64_t)sizeof(int32_t) +
-                          2 * D + (int64_t)sizeof(int32_t);
+    const int64_t per_q = S * CAPQ * (int64_t)(sizeof(uint64_t) + sizeof(int32_t)) + S * (int64_t)sizeof(int32_t);
     int64_t chunk = CAND_BUDGET / per_q;
     chunk = chunk < QG ? QG : chunk / QG * QG;
     if (chunk > nq) chunk = cdiv(nq, QG) * QG;
     if (S * cdiv(chunk, QG) > INT32_MAX) return st::fail(ST_ERR_INVALID, "probe: too many centroids");
     char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, (size_t)(chunk * per_q), s));
     if (!base) return st::scratch_status();
-    // [query digit tiles][candidate keys][candidate ids][counts][query exponents]
-    int8_t *qdig = reinterpret_cast<int8_t *>(base);
-    uint64_t *ck = reinterpret_cast<uint64_t *>(base + chunk * 2 * D);
+    // [candidate keys][candidate ids][counts]
+    uint64_t *ck = reinterpret_cast<uint64_t *>(base);
     int32_t *ci = reinterpret_cast<int32_t *>(ck + chunk * S * CAPQ);
     int32_t *pcnt = ci + chunk * S * CAPQ;
-    int32_t *qex = pcnt + chunk * S;
 
     for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
         const int64_t nqc = nq - q0 < chunk ? nq - q0 : chunk;
         const int64_t gy = cdiv(nqc, QG);
-        st_status st = launch_prep(queries + q0 * D, nqc, qdig, qex, nullptr, s);
-        if (st != ST_OK) return st;
-        hipLaunchKernelGGL(k_probe_part, dim3((unsigned)(S * gy)), dim3(PART_T), 0, s, qdig, qex, (int32_t)nqc, digits,
+        hipLaunchKernelGGL(k_probe_part, dim3((unsigned)(S * gy)), dim3(PART_T), 0, s, queries + q0 * D, (int32_t)nqc, digits,
                            cexp, cnorm, (int32_t)nlist, (int32_t)S, (int32_t)gy, (int32_t)nprobe, ck, ci, pcnt);
         ST_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_probe_merge, dim3((unsigned)cdiv(nqc, 4)), dim3(256), 0, s, ck, ci, pcnt, (int32_t)nqc,
+        hipLaunchKernelGGL(k_probe_merge, dim3((unsigned)nqc), dim3(64), 0, s, ck, ci, pcnt, (int32_t)nqc,
                            (int32_t)S, (int32_t)nprobe, probes + q0 * nprobe);
         ST_LAUNCH_CHECK();
     }
