@@ -310,6 +310,14 @@ st_status st_peak_mfma(int32_t kind, int64_t iters, int32_t blocks, float *sink,
  * nontemporal loads; `sink` as for st_peak_mfma. */
 st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks, float *sink, st_stream stream);
 
+/* Checks the cross-lane exchanges the kernels use (DPP and v_permlane swaps in
+ * place of ds_bpermute) on the current device: `out` (device, 10 x 64
+ * uint32) gets, for one wave, rows 0..7 the exchange of v = 1000 + 7 lane
+ * across lane ^ J for J = 1, 2, 4, 8, 15, 16, 32, 63 (expected 1000 + 7
+ * (lane ^ J)), row 8 the inclusive wave scan of 3 lane + 1 + lane % 5, row 9
+ * lane 37's v in every lane. */
+st_status st_lane_selftest(uint32_t *out, st_stream stream);
+
 /* ---- Misc ---------------------------------------------------------------- */
 
 /* Message of the last failed call on this thread ("" if none). */

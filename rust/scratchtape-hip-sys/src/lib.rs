@@ -328,6 +328,7 @@ extern "C" {
     pub fn st_peak_mfma(kind: i32, iters: i64, blocks: i32, sink: *mut f32, stream: st_stream) -> st_status;
     pub fn st_peak_read(src: *const c_void, bytes: i64, blocks: i32, sink: *mut f32, stream: st_stream)
         -> st_status;
+    pub fn st_lane_selftest(out: *mut u32, stream: st_stream) -> st_status;
     /// The message of the calling thread's last failed call.
     pub fn st_last_error() -> *const c_char;
     /// Synchronises and frees the split-k scratch arena, current and superseded buffers.

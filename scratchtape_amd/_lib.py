@@ -79,6 +79,7 @@ SIGNATURES = {
     "st_device_info": [_vp, _vp, _vp, _vp],
     "st_peak_mfma": [_i32, _i64, _i32, _vp, _vp],
     "st_peak_read": [_vp, _i64, _i32, _vp, _vp],
+    "st_lane_selftest": [_vp, _vp],
     "st_last_error": [],
     "st_sync": [_vp],
     "st_scratch_release": [],

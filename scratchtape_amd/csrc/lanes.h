@@ -15,7 +15,7 @@
 //              swap returns (v with the odd rows / upper half replaced,
 //              v with the even rows / lower half replaced), and a lane takes
 //              the one holding its partner's value.
-// Each of these was checked on the device against lane ^ j.  Inside an
+// Each of these is checked on the device against lane ^ j by st_lane_selftest.  Inside an
 // unrolled loop j is a constant and the switch folds away; any other j falls
 // back to __shfl_xor.  Every lane of the wave must be active (as for a DPP
 // butterfly in general): callers use these in wave-uniform code only.
@@ -82,7 +82,7 @@ __device__ __forceinline__ double xor_lane(double v, int j, int lane) {
 // Inclusive prefix sum over the wave's 64 lanes: DPP row_shr 1, 2, 4, 8
 // within each row of 16 (a shift past the row's start reads 0), then
 // row_bcast:15 adds each even row's last lane to the row after it (rows 1, 3)
-// and row_bcast:31 adds lane 31 to rows 2 and 3.  Checked on the device.
+// and row_bcast:31 adds lane 31 to rows 2 and 3.  Checked by st_lane_selftest.
 __device__ __forceinline__ int32_t wave_incl_scan(int32_t x) {
     x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
     x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);

@@ -4,6 +4,7 @@
 // kernel in the key scans' launch shape, and the device's CU count and clocks.  The benchmark reports these
 // beside the published peaks it prices every kernel against.
 #include "common.h"
+#include "lanes.h"
 
 namespace {
 
@@ -121,6 +122,20 @@ __global__ __launch_bounds__(RT) void k_peak_read(const float4 *__restrict__ src
     if (acc == NEVER) sink[blockIdx.x] = acc;
 }
 
+// One wave: row r < 8 of out gets xor_lane(1000 + 7 lane, J[r], lane) for
+// J = 1, 2, 4, 8, 15, 16, 32, 63 (lane ^ J's value, 1000 + 7 (lane ^ J));
+// row 8 the inclusive wave scan of 3 lane + 1 + lane % 5; row 9 lane 37's
+// value broadcast by lane_value.
+__global__ __launch_bounds__(64) void k_lane_selftest(uint32_t *__restrict__ out) {
+    const int lane = threadIdx.x;
+    const uint32_t v = 1000u + 7u * (uint32_t)lane;
+    constexpr int J[8] = {1, 2, 4, 8, 15, 16, 32, 63};
+#pragma unroll
+    for (int r = 0; r < 8; r++) out[r * 64 + lane] = st::xor_lane(v, J[r], lane);
+    out[8 * 64 + lane] = (uint32_t)st::wave_incl_scan(3 * lane + 1 + lane % 5);
+    out[9 * 64 + lane] = st::lane_value(v, 37);
+}
+
 }  // namespace
 
 extern "C" st_status st_device_info(int32_t *cus, int32_t *clock_khz, int32_t *mem_clock_khz,
@@ -160,6 +175,15 @@ extern "C" st_status st_peak_read(const void *src, int64_t bytes, int32_t blocks
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     hipLaunchKernelGGL(k_peak_read, dim3((unsigned)blocks), dim3(RT), 0, st::stream_of(stream),
                        reinterpret_cast<const float4 *>(src), bytes / 16, sink);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}
+
+extern "C" st_status st_lane_selftest(uint32_t *out, st_stream stream) {
+    st::clear_error();
+    if (!out) return st::fail(ST_ERR_INVALID, "lane_selftest: NULL output");
+    if (!st::device_ok()) return ST_ERR_NO_DEVICE;
+    hipLaunchKernelGGL(k_lane_selftest, dim3(1), dim3(64), 0, st::stream_of(stream), out);
     ST_LAUNCH_CHECK();
     return ST_OK;
 }

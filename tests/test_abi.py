@@ -145,6 +145,7 @@ def test_ceiling_probe_arguments_are_validated():
     assert L.st_peak_mfma(0, 0, 8, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_peak_read(fake, 24, 8, fake, None) == _lib.ST_ERR_INVALID
     assert L.st_peak_read(fake + 4, 32, 8, fake, None) == _lib.ST_ERR_INVALID
+    assert L.st_lane_selftest(None, None) == _lib.ST_ERR_INVALID
     assert L.st_device_info(None, None, None, None) == _lib.ST_ERR_INVALID
 
 

@@ -35,3 +35,21 @@ def test_read_probe_runs_and_leaves_the_sink():
         _lib.call("st_peak_read", buf.data_ptr(), nbytes, 96, sink.data_ptr(), s.cuda_stream)
     torch.cuda.synchronize()
     assert torch.count_nonzero(sink).item() == 0
+
+
+def test_lane_exchanges_match_lane_xor_on_this_device():
+    """The DPP / v_permlane exchanges, the DPP wave scan and the readlane broadcast that the probe, scan,
+    LayerNorm and attention kernels use in place of ds_bpermute give exactly lane ^ J's value, the running sum
+    and lane 37's value."""
+    out = torch.zeros(10 * 64, dtype=torch.int32, device="cuda")
+    _lib.call("st_lane_selftest", out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    got = out.view(10, 64).cpu().numpy().astype("int64")
+    lane = list(range(64))
+    for r, j in enumerate((1, 2, 4, 8, 15, 16, 32, 63)):
+        assert got[r].tolist() == [1000 + 7 * (l ^ j) for l in lane], j
+    run, acc = [], 0
+    for l in lane:
+        acc += 3 * l + 1 + l % 5
+        run.append(acc)
+    assert got[8].tolist() == run
+    assert got[9].tolist() == [1000 + 7 * 37] * 64

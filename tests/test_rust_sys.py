@@ -14,11 +14,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "scratchtape_hip.h")
 CRATE = os.path.join(ROOT, "rust", "scratchtape-hip-sys")
 
-C_SCALARS = {"int32_t": "i32", "int64_t": "i64", "uint64_t": "u64", "uint8_t": "u8", "int8_t": "i8",
+C_SCALARS = {"int32_t": "i32", "int64_t": "i64", "uint64_t": "u64", "uint32_t": "u32", "uint8_t": "u8", "int8_t": "i8",
              "float": "f32", "double": "f64", "void": "c_void", "char": "c_char",
              "st_status": "st_status", "st_stream": "st_stream", "st_matref": "st_matref",
              "st_epilogue": "st_epilogue", "st_gemm": "st_gemm"}
-SIZES = {"i32": 4, "i64": 8, "u64": 8, "f32": 4, "f64": 8, "st_status": 4, "st_stream": 8}
+SIZES = {"i32": 4, "i64": 8, "u64": 8, "u32": 4, "f32": 4, "f64": 8, "st_status": 4, "st_stream": 8}
 
 
 def strip_c_comments(text):
