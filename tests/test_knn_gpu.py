@@ -103,6 +103,34 @@ def test_search_many_cells_and_sixteen_probes(dev):
         check_search(dev, store, codes, scales, cs, queries, probes, k)
 
 
+def test_search_skips_probe_ids_outside_the_cells(dev):
+    # A probe id < 0 or >= ncells is skipped (the header's contract).  The oracle sees each row with those ids
+    # replaced by a repeat of one of its valid ids (a repeated cell is scanned once), or, for a row with none, by
+    # an empty cell.
+    rng = np.random.default_rng(41)
+    ncells = 50
+    sizes = rng.integers(50, 400, ncells)
+    sizes[7] = 0
+    store, codes, scales, cs = make_store(dev, sizes, 43)
+    nq = 12
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, 8, replace=False) for _ in range(nq)]).astype(np.int32)
+    probes[0, 2] = -1
+    probes[1, 0] = ncells
+    probes[1, 5] = 1 << 30
+    probes[2, :] = -1
+    probes[3, ::2] = -7
+    seen = probes.copy()
+    for row in seen:
+        valid = [c for c in row if 0 <= c < ncells]
+        row[(row < 0) | (row >= ncells)] = valid[0] if valid else 7
+    idx, dist = store.search_ivf(torch.from_numpy(queries).to(dev), torch.from_numpy(probes).to(dev), 128)
+    widx, wdist = oracle.knn_search(codes, scales, cs, queries, seen, 128)
+    np.testing.assert_array_equal(idx.cpu().numpy(), widx)
+    np.testing.assert_array_equal(dist.cpu().numpy(), wdist)
+    assert np.all(idx.cpu().numpy()[2] == -1)
+
+
 def test_search_many_queries_sharing_cells(dev):
     # 600 queries x 8 probes over 100 cells: every cell is probed by ~48 queries.
     rng = np.random.default_rng(31)
