@@ -17,8 +17,10 @@
 //              the one holding its partner's value.
 // Each of these is checked on the device against lane ^ j by st_lane_selftest.  Inside an
 // unrolled loop j is a constant and the switch folds away; any other j falls
-// back to __shfl_xor.  Every lane of the wave must be active (as for a DPP
-// butterfly in general): callers use these in wave-uniform code only.
+// back to __shfl_xor.  The partner lane must be active (a DPP read from a
+// disabled lane does not return its register): callers use these in
+// wave-uniform code, or (j < 16, which stays within a row of 16 lanes) in code
+// uniform over each row.
 #pragma once
 
 #include <hip/hip_runtime.h>
