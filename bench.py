@@ -889,7 +889,7 @@ def main():
             sys.exit(3)
         pms, ptiming = pb.run(stream, args.steps, args.warmup)
         probe = dict(ms_per_batch=round(pms, 5), **ptiming, queries_per_s=round(pb.NQ / pms * 1e3, 1),
-                     roofline=roofline("st_knn_probe (k_probe_prep + k_probe_part + k_probe_merge)", pb.ops,
+                     roofline=roofline("st_knn_probe (k_probe_part + k_probe_merge)", pb.ops,
                                        pb.bytes, pms,
                                        traffic_for("st_knn_probe", "scratchtape_amd/csrc/knn_probe.hip"), route="i8"))
         if not args.no_cpu:

@@ -505,7 +505,12 @@ __device__ __forceinline__ int slot_entry(int32_t c, int e) {
 
 __device__ __forceinline__ int slot_size(int32_t c) { return (c & 0xffff) + ((c >> 16) & 0xffff); }
 
-constexpr int MREG = 24;  // candidates per lane held in registers by the merge
+// Candidates per lane held in registers by the merge: the first and last 16
+// entries of its slot.  With 12 + 12, one query in ~30 of the benchmark's
+// batch had a slot end past it and took the general path (twice as long, and
+// the whole launch waited for it); 16 + 16 keeps the arrays in registers (at
+// 20 + 20 the compiler moves them to scratch memory).
+constexpr int MREG = 32;
 
 // One wave per query (a workgroup of one wave, so the queries spread over
 // every CU): probes[q][0, nprobe) by (key, id)
