@@ -1065,7 +1065,7 @@ namespace {
 // longer than SCHED_MAX.  Which workgroup runs a unit never changes its
 // arithmetic.  The last schedule is kept per host thread with the shapes it
 // was made for, so a group issued again with the same shapes reuses it.
-constexpr int EPI_STAGES = 2;
+constexpr int EPI_STAGES = 4;  // a 256 x 128 unit's epilogue: ~6-7 k cycles, ~4 stages of ~1,750
 
 void schedule(GroupArgs &ga, int L) {
     thread_local std::vector<int32_t> last_key;
