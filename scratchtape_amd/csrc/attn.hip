@@ -171,6 +171,72 @@ __device__ __forceinline__ half8 frag_t(const _Float16 *xt, int ldt, int row, in
     return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// The LDS operands of one pair of 16-row query tiles (2 mm, 2 mm + 1) for a dK / dV wave: the
+// A operands of S and dP (rows of Q and dO), of dV and dK (the pair's columns of dO^T and Q^T),
+// and L (in log2 units) and D of the 8 queries a lane holds.
+template <int NB>
+struct KvPair {
+    half8 q[4], d[4], dt[4], qt[4];
+    float l[8], dd[8];
+    // Tile 2 mm + w2: its S and dP A operands, L and D.
+    __device__ __forceinline__ void fetch_tile(int mm, int w2, const _Float16 *sQ, const _Float16 *sO,
+                                               const float *sL, const float *sD, int li, int g) {
+        constexpr int KP = Split<NB, 1>::KP;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            q[2 * w2 + c] = frag_r(sQ, KP, 16 * (2 * mm + w2) + li, c, g);
+            d[2 * w2 + c] = frag_r(sO, KP, 16 * (2 * mm + w2) + li, c, g);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int qq = 16 * (2 * mm + w2) + 4 * g + r;
+            l[4 * w2 + r] = sL[qq];
+            dd[4 * w2 + r] = sD[qq];
+        }
+    }
+    // The pair's dV and dK A operands.
+    __device__ __forceinline__ void fetch_cols(int mm, const _Float16 *sQt, const _Float16 *sOt, int li, int g) {
+        constexpr int LDT = Split<NB, 1>::LDT;
+#pragma unroll
+        for (int ht = 0; ht < 4; ht++) {
+            dt[ht] = frag_t(sOt, LDT, 16 * ht + li, mm, g);
+            qt[ht] = frag_t(sQt, LDT, 16 * ht + li, mm, g);
+        }
+    }
+    __device__ __forceinline__ void fetch(int mm, const _Float16 *sQ, const _Float16 *sO, const _Float16 *sQt,
+                                          const _Float16 *sOt, const float *sL, const float *sD, int li, int g) {
+        fetch_tile(mm, 0, sQ, sO, sL, sD, li, g);
+        fetch_tile(mm, 1, sQ, sO, sL, sD, li, g);
+        fetch_cols(mm, sQt, sOt, li, g);
+    }
+};
+
+// The LDS operands of one pair of 16-row key tiles (2 mm, 2 mm + 1) for a dQ wave: the A
+// operands of S^T and dP^T (rows of K and V) and of dQ (the pair's columns of K^T).
+template <int NB>
+struct QPair {
+    half8 k[4], v[4], kt[4];
+    __device__ __forceinline__ void fetch_tile(int mm, int w2, const _Float16 *sK, const _Float16 *sV, int li, int g) {
+        constexpr int KP = Split<NB, 1>::KP;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            k[2 * w2 + c] = frag_r(sK, KP, 16 * (2 * mm + w2) + li, c, g);
+            v[2 * w2 + c] = frag_r(sV, KP, 16 * (2 * mm + w2) + li, c, g);
+        }
+    }
+    __device__ __forceinline__ void fetch_cols(int mm, const _Float16 *sKt, int li, int g) {
+        constexpr int LDT = Split<NB, 1>::LDT;
+#pragma unroll
+        for (int ht = 0; ht < 4; ht++) kt[ht] = frag_t(sKt, LDT, 16 * ht + li, mm, g);
+    }
+    __device__ __forceinline__ void fetch(int mm, const _Float16 *sK, const _Float16 *sV, const _Float16 *sKt, int li,
+                                          int g) {
+        fetch_tile(mm, 0, sK, sV, li, g);
+        fetch_tile(mm, 1, sK, sV, li, g);
+        fetch_cols(mm, sKt, li, g);
+    }
+};
+
 // Workgroup id -> (problem z, unit u in [0, U)), placing all U units of a
 // problem on one XCD (workgroups are dealt to the 8 XCDs round robin), so the
 // operands that both backward roles stage are read from one L2:
@@ -312,6 +378,9 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
                                                             int32_t h, int64_t nz, float scale) {
     using S = SplitB<NB>;
     constexpr int T = S::T, KP = S::KP, LDT = S::LDT;
+    // Each wave reads the next tile pair's LDS operands while it multiplies the current one, where
+    // the registers allow: up to 8 waves a workgroup (2 a SIMD); more waves would spill them.
+    constexpr bool PF = NB <= 8;
     const float sl2 = scale * LOG2E;
     // dK/dV units: Q, dO row-major, Q^T, dO^T; dQ units: K, V row-major, K^T.
     __shared__ _Float16 sR0[T * KP], sR1[T * KP];
@@ -350,35 +419,46 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             f32x4 dv[4], dk[4];
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) dv[ht] = dk[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // Query-tile pairs m0 .. NB/2 - 1 (tiles 2 mm, 2 mm + 1; a tile before the key block
+            // masks to zero), each pair's LDS operands read while the pair before it runs:
+            // buffer mm % 2 holds pair mm.
+            const int m0 = kb >> 1;
+            KvPair<NB> f[PF ? 2 : 1];
+            if constexpr (PF) {
+                if (m0 & 1)
+                    f[1].fetch(m0, sR0, sR1, sT0, sT1, sL, sD, li, g);
+                else
+                    f[0].fetch(m0, sR0, sR1, sT0, sT1, sL, sD, li, g);
+            }
 #pragma unroll
             for (int mm = 0; mm < NB / 2; mm++) {
-                if (2 * mm + 1 < kb) continue;  // both query tiles precede the key block
+                if (mm < m0) continue;
+                KvPair<NB> &c = f[PF ? (mm & 1) : 0];
+                if constexpr (PF) {
+                    if (mm + 1 < NB / 2) f[(mm + 1) & 1].fetch(mm + 1, sR0, sR1, sT0, sT1, sL, sD, li, g);
+                }
                 half8 pb, sb;
 #pragma unroll
                 for (int w2 = 0; w2 < 2; w2++) {
-                    const int qt = 2 * mm + w2;
-                    if (qt < kb) {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) pb[4 * w2 + r] = sb[4 * w2 + r] = (_Float16)0.f;
-                        continue;
-                    }
+                    if constexpr (!PF) c.fetch_tile(mm, w2, sR0, sR1, sL, sD, li, g);
                     // S = Q K^T and dP = dO V^T: lane holds queries 16 qt + 4 g + r of its key.
-                    f32x4 sv = mfma(frag_r(sR0, KP, 16 * qt + li, 0, g), k0, f32x4{0.f, 0.f, 0.f, 0.f});
-                    sv = mfma(frag_r(sR0, KP, 16 * qt + li, 1, g), k1, sv);
-                    f32x4 dp = mfma(frag_r(sR1, KP, 16 * qt + li, 0, g), v0, f32x4{0.f, 0.f, 0.f, 0.f});
-                    dp = mfma(frag_r(sR1, KP, 16 * qt + li, 1, g), v1, dp);
+                    f32x4 sv = mfma(c.q[2 * w2], k0, f32x4{0.f, 0.f, 0.f, 0.f});
+                    sv = mfma(c.q[2 * w2 + 1], k1, sv);
+                    f32x4 dp = mfma(c.d[2 * w2], v0, f32x4{0.f, 0.f, 0.f, 0.f});
+                    dp = mfma(c.d[2 * w2 + 1], v1, dp);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const int q = 16 * qt + 4 * g + r;
-                        const float p = key <= q ? exp2_(fmaf(sv[r], sl2, -sL[q])) : 0.f;
+                        const int q = 16 * (2 * mm + w2) + 4 * g + r;
+                        const float p = key <= q ? exp2_(fmaf(sv[r], sl2, -c.l[4 * w2 + r])) : 0.f;
                         pb[4 * w2 + r] = (_Float16)p;
-                        sb[4 * w2 + r] = (_Float16)(p * (dp[r] - sD[q]) * scale);
+                        sb[4 * w2 + r] = (_Float16)(p * (dp[r] - c.dd[4 * w2 + r]) * scale);
                     }
                 }
+                if constexpr (!PF) c.fetch_cols(mm, sT0, sT1, li, g);
 #pragma unroll
                 for (int ht = 0; ht < 4; ht++) {
-                    dv[ht] = mfma(frag_t(sT1, LDT, 16 * ht + li, mm, g), pb, dv[ht]);
-                    dk[ht] = mfma(frag_t(sT0, LDT, 16 * ht + li, mm, g), sb, dk[ht]);
+                    dv[ht] = mfma(c.dt[ht], pb, dv[ht]);
+                    dk[ht] = mfma(c.qt[ht], sb, dk[ht]);
                 }
             }
             float *gr = gbase + (int64_t)key * ld;
@@ -427,32 +507,37 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             f32x4 dq[4];
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) dq[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // Key-tile pairs 0 .. qb / 2 (a tile past the query block masks to zero), each
+            // pair's LDS operands read while the pair before it runs: buffer mm % 2 holds pair mm.
+            const int m1 = qb >> 1;
+            QPair<NB> f[PF ? 2 : 1];
+            if constexpr (PF) f[0].fetch(0, sR0, sR1, sT0, li, g);
 #pragma unroll
             for (int mm = 0; mm < NB / 2; mm++) {
-                if (2 * mm > qb) continue;
+                if (mm > m1) continue;
+                QPair<NB> &c = f[PF ? (mm & 1) : 0];
+                if constexpr (PF) {
+                    if (mm + 1 < NB / 2 && mm + 1 <= m1) f[(mm + 1) & 1].fetch(mm + 1, sR0, sR1, sT0, li, g);
+                }
                 half8 sb;
 #pragma unroll
                 for (int w2 = 0; w2 < 2; w2++) {
-                    const int kt = 2 * mm + w2;
-                    if (kt > qb) {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) sb[4 * w2 + r] = (_Float16)0.f;
-                        continue;
-                    }
+                    if constexpr (!PF) c.fetch_tile(mm, w2, sR0, sR1, li, g);
                     // S^T = K Q^T and dP^T = V dO^T: lane holds keys 16 kt + 4 g + r of its query.
-                    f32x4 st = mfma(frag_r(sR0, KP, 16 * kt + li, 0, g), q0, f32x4{0.f, 0.f, 0.f, 0.f});
-                    st = mfma(frag_r(sR0, KP, 16 * kt + li, 1, g), q1, st);
-                    f32x4 dpt = mfma(frag_r(sR1, KP, 16 * kt + li, 0, g), d0, f32x4{0.f, 0.f, 0.f, 0.f});
-                    dpt = mfma(frag_r(sR1, KP, 16 * kt + li, 1, g), d1, dpt);
+                    f32x4 st = mfma(c.k[2 * w2], q0, f32x4{0.f, 0.f, 0.f, 0.f});
+                    st = mfma(c.k[2 * w2 + 1], q1, st);
+                    f32x4 dpt = mfma(c.v[2 * w2], d0, f32x4{0.f, 0.f, 0.f, 0.f});
+                    dpt = mfma(c.v[2 * w2 + 1], d1, dpt);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const int key = 16 * kt + 4 * g + r;
+                        const int key = 16 * (2 * mm + w2) + 4 * g + r;
                         const float p = key <= q ? exp2_(fmaf(st[r], sl2, -L)) : 0.f;
                         sb[4 * w2 + r] = (_Float16)(p * (dpt[r] - dsum) * scale);
                     }
                 }
+                if constexpr (!PF) c.fetch_cols(mm, sT0, li, g);
 #pragma unroll
-                for (int ht = 0; ht < 4; ht++) dq[ht] = mfma(frag_t(sT0, LDT, 16 * ht + li, mm, g), sb, dq[ht]);
+                for (int ht = 0; ht < 4; ht++) dq[ht] = mfma(c.kt[ht], sb, dq[ht]);
             }
             float *gr = gbase + (int64_t)q * ld;
 #pragma unroll
