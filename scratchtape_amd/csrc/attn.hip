@@ -94,10 +94,14 @@ template <int NB>
 using SplitB = Split<NB, 1>;
 
 // Block of wave w of workgroup x of a problem, or -1 (a wave without a block
-// when the pairs do not split evenly).
+// when the pairs do not split evenly).  With G = 1 the first NB / 2 waves take
+// blocks 0, 1, .. and the rest take NB - 1, NB - 2, ..: a workgroup's waves are
+// dealt to the CU's 4 SIMDs in turn, so for NB = 8 the two waves on a SIMD hold
+// blocks p and NB - 1 - p, which carry NB / 2 + 1 tile pairs between them in
+// either backward role (a SIMD's waves share its matrix core and issue slots).
 template <int NB, int G>
 __device__ __forceinline__ int block_of(int w, int x) {
-    if constexpr (G == 1) return w;
+    if constexpr (G == 1) return w < NB / 2 ? w : 3 * NB / 2 - 1 - w;
     const int p = 2 * (w >> 1) + x;
     return p < NB / 2 ? ((w & 1) ? NB - 1 - p : p) : -1;
 }
@@ -419,23 +423,19 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             f32x4 dv[4], dk[4];
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) dv[ht] = dk[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
-            // Query-tile pairs m0 .. NB/2 - 1 (tiles 2 mm, 2 mm + 1; a tile before the key block
-            // masks to zero), each pair's LDS operands read while the pair before it runs:
-            // buffer mm % 2 holds pair mm.
+            // Query-tile pairs NB/2 - 1 down to m0 (tiles 2 mm, 2 mm + 1; a tile before the key
+            // block masks to zero), so every wave starts on the same code; each pair's LDS
+            // operands are read while the pair before it runs (buffer i % 2 holds the i-th).
             const int m0 = kb >> 1;
             KvPair<NB> f[PF ? 2 : 1];
-            if constexpr (PF) {
-                if (m0 & 1)
-                    f[1].fetch(m0, sR0, sR1, sT0, sT1, sL, sD, li, g);
-                else
-                    f[0].fetch(m0, sR0, sR1, sT0, sT1, sL, sD, li, g);
-            }
+            if constexpr (PF) f[0].fetch(NB / 2 - 1, sR0, sR1, sT0, sT1, sL, sD, li, g);
 #pragma unroll
-            for (int mm = 0; mm < NB / 2; mm++) {
-                if (mm < m0) continue;
-                KvPair<NB> &c = f[PF ? (mm & 1) : 0];
+            for (int i = 0; i < NB / 2; i++) {
+                const int mm = NB / 2 - 1 - i;
+                if (mm < m0) break;
+                KvPair<NB> &c = f[PF ? (i & 1) : 0];
                 if constexpr (PF) {
-                    if (mm + 1 < NB / 2) f[(mm + 1) & 1].fetch(mm + 1, sR0, sR1, sT0, sT1, sL, sD, li, g);
+                    if (mm - 1 >= m0) f[(i + 1) & 1].fetch(mm - 1, sR0, sR1, sT0, sT1, sL, sD, li, g);
                 }
                 half8 pb, sb;
 #pragma unroll
@@ -514,7 +514,7 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             if constexpr (PF) f[0].fetch(0, sR0, sR1, sT0, li, g);
 #pragma unroll
             for (int mm = 0; mm < NB / 2; mm++) {
-                if (mm > m1) continue;
+                if (mm > m1) break;
                 QPair<NB> &c = f[PF ? (mm & 1) : 0];
                 if constexpr (PF) {
                     if (mm + 1 < NB / 2 && mm + 1 <= m1) f[(mm + 1) & 1].fetch(mm + 1, sR0, sR1, sT0, li, g);
