@@ -250,11 +250,18 @@ __device__ __forceinline__ QInfo quantize_query(const float *qrow, int lane, int
         sq2 += (double)Q * (double)Q;
         sQ[4 * lane + t] = (int16_t)Q;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
+    // Butterfly over the wave, written out so that every distance is a constant (a loop here is
+    // not unrolled, and a run-time distance would take the ds_bpermute path).
+    auto fold = [&](int o) __attribute__((always_inline)) {
         sq += st::xor_lane(sq, o, lane);
         sq2 += st::xor_lane(sq2, o, lane);
-    }
+    };
+    fold(32);
+    fold(16);
+    fold(8);
+    fold(4);
+    fold(2);
+    fold(1);
     return QInfo{qs, (float)sq2 * (qs * qs), sq};
 }
 
