@@ -36,10 +36,13 @@
 // its waves share into LDS as f16 (row-major and, where an operand is needed
 // transposed, V^T, Q^T, dO^T or K^T) once per problem, with every load of a
 // thread in flight at once; the MFMA loops then read only LDS and registers.
-// Causal work is uneven across the waves (block j has j + 1 tiles), so the
-// critical path is the last block's NB tiles; at T = 128 two waves share a
-// SIMD and the short blocks' waves fill the gaps of the long ones.  Two 16-row tiles form the 32-deep k-chunk
-// of an MFMA whose contraction runs over rows: element e of lane group g is
+// Causal work is uneven across the waves (block j has j + 1 tiles); at T = 128
+// two waves share a SIMD, and the backward gives them blocks p and NB - 1 - p
+// so that every SIMD carries the same number of tile pairs (block_of).  The
+// outputs leave through nontemporal stores, so that they stream out as the
+// waves finish rather than wait in L2 for the end-of-kernel write-back.  Two
+// 16-row tiles form the 32-deep k-chunk of an MFMA whose contraction runs over
+// rows: element e of lane group g is
 // row 4g + e of the first tile (e < 4) or of the second (e >= 4), the order in
 // which the 16x16 accumulator layout hands them out; A and B agree on it.
 #include "common.h"
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(SplitF<NB>::NT) void k_attn_fwd(const float *__rest
         }
         float *orow = ctx + (bb * T + q) * D + hh * HD;
 #pragma unroll
-        for (int ht = 0; ht < 4; ht++) *reinterpret_cast<f32x4 *>(orow + 16 * ht + 4 * g) = o[ht];
+        for (int ht = 0; ht < 4; ht++) __builtin_nontemporal_store(o[ht], reinterpret_cast<f32x4 *>(orow + 16 * ht + 4 * g));
         if (g == 0) lse[z * T + q] = (m + __log2f(sum)) * LN2;
     }
 }
@@ -464,8 +467,8 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             float *gr = gbase + (int64_t)key * ld;
 #pragma unroll
             for (int ht = 0; ht < 4; ht++) {
-                *reinterpret_cast<f32x4 *>(gr + D + 16 * ht + 4 * g) = dk[ht];
-                *reinterpret_cast<f32x4 *>(gr + 2 * D + 16 * ht + 4 * g) = dv[ht];
+                __builtin_nontemporal_store(dk[ht], reinterpret_cast<f32x4 *>(gr + D + 16 * ht + 4 * g));
+                __builtin_nontemporal_store(dv[ht], reinterpret_cast<f32x4 *>(gr + 2 * D + 16 * ht + 4 * g));
             }
         }
     } else {
@@ -541,7 +544,7 @@ __global__ __launch_bounds__(SplitB<NB>::NT) void k_attn_bwd(const float *__rest
             }
             float *gr = gbase + (int64_t)q * ld;
 #pragma unroll
-            for (int ht = 0; ht < 4; ht++) *reinterpret_cast<f32x4 *>(gr + 16 * ht + 4 * g) = dq[ht];
+            for (int ht = 0; ht < 4; ht++) __builtin_nontemporal_store(dq[ht], reinterpret_cast<f32x4 *>(gr + 16 * ht + 4 * g));
         }
     }
 }

@@ -231,7 +231,12 @@ __global__ __launch_bounds__(256) void k_ln_bwd_sum(const float *__restrict__ pa
 constexpr int LNV_ROWS = 16;  // rows per backward workgroup (4 per wave)
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+// Output rows (y, dx) through nontemporal stores: they stream out as the
+// waves finish instead of waiting in L2 for the end-of-kernel write-back.
+typedef float lnf4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st4(float *p, float4 v) {
+    __builtin_nontemporal_store(lnf4{v.x, v.y, v.z, v.w}, reinterpret_cast<lnf4 *>(p));
+}
 
 // grid: ceil(rows / 4) workgroups of 4 row-waves.  The formulas of k_ln_fwd;
 // a lane adds its four columns pairwise before the butterfly, so the row sums
