@@ -797,7 +797,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
 
     // The epilogue of cur, straight from the accumulators: lane l holds
     // column l % 32 of each 32 x 32 block and rows 8 (e / 4) + 4 (l / 32) +
-    // e % 4 of it.
+    // e % 4 of it.  The stores are nontemporal (the outputs are not read again
+    // by this kernel; the step set measured ~1 % faster than with plain stores).
     auto epilogue = [&]() __attribute__((always_inline)) {
         const GProb &g = sga.p[cur.p];
         const int gflags = uni(g.flags), gsplits = uni(g.splits);
@@ -853,7 +854,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
                     }
                 }
 #pragma unroll
-                for (int e = 0; e < 16; e++) obase[idx(e)] = v[e];
+                for (int e = 0; e < 16; e++) __builtin_nontemporal_store(v[e], obase + idx(e));
             }
         }
         if (cur.cs && id < TN) {
