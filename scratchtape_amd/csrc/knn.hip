@@ -23,7 +23,7 @@
 // chunks in flight (two waves per SIMD with up to 256 VGPRs each hold more
 // bytes in flight than four waves with 128, and the scoring of one chunk
 // hides behind the loads of the next two; four chunks per wave measured
-// ~0.5 % slower on the 256-query batch, five ~0.3 %).  Scoring runs on the matrix cores: the key codes are FP4
+// ~0.5 % slower on the 256-query batch, five ~0.7 %).  Scoring runs on the matrix cores: the key codes are FP4
 // e2m1 operands as stored (a 2-bit code in the low bits of a nibble is u / 2),
 // the query is four FP8 rows of balanced base-16 digits, and one scaled
 // FP8 x FP4 MFMA per 128 dims gives the exact integer dot of 16 keys; one
