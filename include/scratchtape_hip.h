@@ -327,11 +327,25 @@ const char *st_last_error(void);
  * until exit): waits for every device the library used, then frees all of its
  * scratch arenas, current and superseded.  Only for callers that will not
  * replay again any graph that captured a library call; the next call that
- * needs scratch allocates it anew. */
+ * needs scratch allocates it anew.  It must not run concurrently with any
+ * other library call (another thread's call may hold an arena buffer it has
+ * not yet launched into). */
 st_status st_scratch_release(void);
 
-/* Waits for the work enqueued on `stream`. */
+/* Waits for the work enqueued on `stream`.  It then also checks the current
+ * device for slot waits of the grouped f16 GEMM kernel that gave up (each
+ * wait is bounded so that the kernel always ends; a give-up means its
+ * producer and consumer waves lost step, and the outputs of the grouped f16
+ * GEMMs run since the last check are not valid): ST_ERR_HIP with a message
+ * if there were any, and the count is cleared.  Reference failures surface
+ * as panics (tensor.rs:253, gpu_step/matmul.rs:107). */
 st_status st_sync(st_stream stream);
+
+/* No reference counterpart; for tests of the check above.  Sets how many
+ * times a slot wait of the grouped f16 GEMM kernel polls its counter before
+ * it gives up, for launches enqueued afterwards (process-wide; a negative
+ * value restores the default, 2^20). */
+st_status st_set_wait_limit(int64_t polls);
 
 /* Library version string. */
 const char *st_version(void);

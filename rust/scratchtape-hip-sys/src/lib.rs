@@ -334,6 +334,7 @@ extern "C" {
     /// Synchronises and frees the split-k scratch arena, current and superseded buffers.
     pub fn st_scratch_release() -> st_status;
     pub fn st_sync(stream: st_stream) -> st_status;
+    pub fn st_set_wait_limit(polls: i64) -> st_status;
     pub fn st_version() -> *const c_char;
 }
 

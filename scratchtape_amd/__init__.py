@@ -15,7 +15,7 @@ Python mirrors of the reference interfaces they replace:
 """
 from ._lib import ScratchtapeError, lib  # noqa: F401
 from .matmul import (Epilogue, MatRef, f16_enabled, f16_route, matmul, matmul_f32, matmul_grouped,  # noqa: F401
-                     matmul_with)
+                     matmul_with, set_wait_limit, sync)
 
 __all__ = ["ScratchtapeError", "lib", "MatRef", "Epilogue", "matmul", "matmul_f32", "matmul_with", "matmul_grouped",
-           "f16_enabled", "f16_route"]
+           "f16_enabled", "f16_route", "sync", "set_wait_limit"]

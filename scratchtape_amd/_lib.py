@@ -82,6 +82,7 @@ SIGNATURES = {
     "st_lane_selftest": [_vp, _vp],
     "st_last_error": [],
     "st_sync": [_vp],
+    "st_set_wait_limit": [_i64],
     "st_scratch_release": [],
     "st_version": [],
 }

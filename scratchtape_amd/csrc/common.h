@@ -27,8 +27,9 @@ void clear_error();
 // a graph) and keeps the superseded one until st_scratch_release(), since
 // enqueued work or a captured graph may still use it.  Inside a ScratchScope
 // the scope decides instead: a fixed buffer (sizes beyond it are refused), or
-// private buffers that the scope frees, after a device synchronisation, when
-// it ends.  Returns nullptr and sets the error on failure.
+// private buffers that the scope frees when it ends (its owner synchronises
+// the stream that used them first).  Returns nullptr and sets the error on
+// failure.
 enum ScratchSlot { SCRATCH_SPLITK = 0, SCRATCH_KNN = 1, SCRATCH_ROWS = 2, SCRATCH_SLOTS = 3 };
 void *scratch(ScratchSlot slot, size_t bytes, hipStream_t stream);
 

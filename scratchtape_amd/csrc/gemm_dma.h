@@ -44,5 +44,9 @@ constexpr int GROUP_MAX = 16;
 bool group_eligible(const DmaGemm &g);
 bool group_tall(const DmaGemm &g);
 st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream);
+// Reads and clears the current device's count of grouped-kernel slot waits
+// that gave up; ST_ERR_HIP with a message if there were any.  The caller has
+// synchronised the work it wants covered.
+st_status check_group_waits();
 
 }  // namespace st

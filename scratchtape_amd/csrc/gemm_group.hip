@@ -23,7 +23,9 @@
 // k_sum_group adds in ascending slice order with accumulate and the column
 // sums, as k_sum_slices does (matmul.rs:259-299).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 #include <queue>
 #include <utility>
@@ -83,6 +85,9 @@ struct GroupArgs {
     // 1: owner[x][i] is the workgroup (0 .. L-1 of XCD x's L) that runs unit i
     // of x's list; 0: round robin (workgroup w runs units w, w + L, ..).
     int32_t sched;
+    // Polls of a slot counter after which a wait of the f16 kernel gives up
+    // (and counts the give-up in g_waits_given_up).
+    uint32_t wait_polls;
     uint8_t owner[XCDS][SCHED_MAX];
 };
 static_assert(sizeof(GroupArgs) <= 4000, "kernel arguments");
@@ -485,13 +490,25 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 // writing it).  So neither role waits for the other's whole step: producers
 // keep loading and converting through the consumers' epilogues, up to two
 // stages ahead.
+// Slot waits of k_gemm_group16 that gave up (per device; st_sync reads and
+// clears it).
+__device__ uint32_t g_waits_given_up;
+
 namespace r16 {
 
-// Waits until the LDS counter reaches target (bounded, so that a wave always
-// ends; the protocol reaches every target).
-__device__ __forceinline__ void spin_until(uint32_t *p, uint32_t target) {
-    for (int i = 0; i < (1 << 20); i++) {
+// Waits until the LDS counter reaches target.  The wait is bounded, so that a
+// wave always ends: after `polls` polls it gives up, and since the slot it
+// guards may then be read half-written or overwritten while read, the
+// give-up is counted in g_waits_given_up (a device-memory word, added to with
+// a vector atomic), which st_sync reports as an error.  The protocol reaches
+// every target; a give-up means a fault in it.
+__device__ __forceinline__ void spin_until(uint32_t *p, uint32_t target, uint32_t polls) {
+    for (uint32_t i = 0;; i++) {
         if (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+        if (i >= polls) {
+            if (__lane_id() == 0) atomicAdd(&g_waits_given_up, 1u);
+            return;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -506,7 +523,13 @@ struct Cfg {
     static constexpr int SA = TM * 64, SB = TN * 64;    // bytes of a stage (f16)
     static constexpr int SLOT = SA + SB;
     static constexpr int NS = 5;                        // every unit (split slice) keeps NS - 1 = 4 stages
-    static_assert(NSL * SLOT + NSL * 4 * TN * 4 + sizeof(GroupArgs) + 4 * (st::GROUP_MAX + 1) <= 160 * 1024, "LDS");
+    // The kernel's LDS: NSL + 1 slots (the last for the unused conversion
+    // past the final stage), their column-sum partials, the slot counters,
+    // the group's arguments and their prefix sums.
+    static_assert((NSL + 1) * SLOT + (NSL + 1) * 4 * TN * 4 + 2 * NSL * 4 + sizeof(GroupArgs) +
+                          4 * (st::GROUP_MAX + 1) <=
+                      160 * 1024,
+                  "LDS");
 };
 using Tall16 = Cfg<256>;
 using Square16 = Cfg<128>;
@@ -699,6 +722,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
     load_args(ga, sga, cum, x, tid, C::THREADS);
 
     const int nlist = uni(cum[sga.count]), sched = uni(sga.sched);
+    const uint32_t polls = (uint32_t)uni((int32_t)sga.wait_polls);
     auto next_pos = [&](int prev) __attribute__((always_inline)) -> int {
         if (!sched) return min(prev < 0 ? w : prev + L, nlist);
         for (int base = prev + 1; base < nlist; base += 64) {
@@ -900,7 +924,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
             issue(set_c);
             constexpr int S1 = (S + 1) % NSL;
             const bool none = !(st + 1 < cur.nst) && nxt.p < 0;
-            if (!none) spin_until(&s_empty[S1], 4 * (pc / NSL));
+            if (!none) spin_until(&s_empty[S1], 4 * (pc / NSL), polls);
             convert(std::integral_constant<int, S1>(), 1);
             __builtin_amdgcn_s_waitcnt(0xC07F);
             if (!none && lane == 0)
@@ -916,7 +940,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         // Stage q: multiply slot S.
         auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
             constexpr int S = decltype(set_c)::value;
-            spin_until(&s_full[S], 4 * (cq / NSL + 1));
+            spin_until(&s_full[S], 4 * (cq / NSL + 1), polls);
             const char *slot = lds + S * SLOT;
             half8 af[2][M32], bf[2][N32];
 #pragma unroll
@@ -1020,6 +1044,10 @@ bool can_split(const st::DmaGemm &d) {
     return !d.bias && !d.relu && !d.mask && !d.res && d.ldo == d.n && d.o_group == 1 &&
            (d.batch == 1 || d.o_stride == d.m * d.n);
 }
+
+// Polls before a slot wait of k_gemm_group16 gives up (st_set_wait_limit).
+constexpr uint32_t DEFAULT_WAIT_POLLS = 1u << 20;
+std::atomic<uint32_t> g_wait_polls{DEFAULT_WAIT_POLLS};
 
 int cu_count() {
     int dev = 0, cus = 0;
@@ -1174,6 +1202,7 @@ st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupAr
 
     GroupArgs ga;
     std::memset(&ga, 0, sizeof ga);
+    ga.wait_polls = g_wait_polls.load(std::memory_order_relaxed);
     SumArgs sa;
     std::memset(&sa, 0, sizeof sa);
     int64_t units = 0, sum_threads = 0;
@@ -1257,6 +1286,37 @@ st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupAr
 
 namespace st {
 
+st_status check_group_waits() {
+    constexpr int MAX_DEVICES = 64;
+    static std::mutex mu;
+    static void *word[MAX_DEVICES];  // device address of g_waits_given_up per device
+    int dev = 0;
+    ST_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) return ST_OK;
+    void *p = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!word[dev]) {
+            const hipError_t e = hipGetSymbolAddress(&word[dev], HIP_SYMBOL(g_waits_given_up));
+            if (e != hipSuccess || !word[dev]) {
+                (void)hipGetLastError();
+                word[dev] = nullptr;
+                return fail(ST_ERR_HIP, "hipGetSymbolAddress of the wait counter failed: %s", hipGetErrorString(e));
+            }
+        }
+        p = word[dev];
+    }
+    uint32_t n = 0;
+    ST_HIP_CHECK(hipMemcpy(&n, p, sizeof n, hipMemcpyDeviceToHost));
+    if (n == 0) return ST_OK;
+    const uint32_t zero = 0;
+    ST_HIP_CHECK(hipMemcpy(p, &zero, sizeof zero, hipMemcpyHostToDevice));
+    return fail(ST_ERR_HIP,
+                "grouped GEMM: %u slot wait(s) gave up after %u polls; the outputs of the grouped f16 GEMMs run "
+                "since the last st_sync are not valid",
+                n, g_wait_polls.load(std::memory_order_relaxed));
+}
+
 st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream) {
     if (f16)
         return tall ? launch_group<r16::Tall16>(items, count, &r16::k_gemm_group16<r16::Tall16>, stream)
@@ -1266,3 +1326,10 @@ st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipSt
 }
 
 }  // namespace st
+
+extern "C" st_status st_set_wait_limit(int64_t polls) {
+    st::clear_error();
+    if (polls > (int64_t)UINT32_MAX) return st::fail(ST_ERR_INVALID, "wait limit %lld too large", (long long)polls);
+    g_wait_polls.store(polls < 0 ? DEFAULT_WAIT_POLLS : (uint32_t)polls, std::memory_order_relaxed);
+    return ST_OK;
+}

@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gemm_dma.h"
 
 namespace st {
 
@@ -42,12 +43,13 @@ ScratchScope::ScratchScope(void *fixed, size_t bytes) : fixed_(fixed), fixed_byt
 
 ScratchScope::ScratchScope() : prev_(g_scope) { g_scope = this; }
 
+// The owner of a private scope has synchronised the stream its work went to
+// before the scope ends (st_ndarray_matmul does), so the buffers are idle:
+// no device-wide synchronisation, which would also wait for other threads'
+// streams.
 ScratchScope::~ScratchScope() {
     g_scope = prev_;
-    if (!owned_.empty()) {
-        (void)hipDeviceSynchronize();
-        for (void *p : owned_) (void)hipFree(p);
-    }
+    for (void *p : owned_) (void)hipFree(p);
 }
 
 void *scratch(ScratchSlot slot, size_t bytes, hipStream_t stream) {
@@ -148,7 +150,7 @@ extern "C" const char *st_last_error(void) { return st::g_error.c_str(); }
 extern "C" st_status st_sync(st_stream stream) {
     st::clear_error();
     ST_HIP_CHECK(hipStreamSynchronize(st::stream_of(stream)));
-    return ST_OK;
+    return st::check_group_waits();
 }
 
 extern "C" st_status st_scratch_release(void) {

@@ -143,3 +143,14 @@ def f16_enabled() -> bool:
 def f16_route(m: int, k: int, n: int, col_sum: bool = False, b_trans: bool = False) -> bool:
     """Whether a shape takes the f16 route (matmul.rs:108-112, 524-534)."""
     return not (col_sum and b_trans) and k > 0 and k % 32 == 0 and m % 64 == 0 and n % 32 == 0
+
+
+def sync(stream=None) -> None:
+    """st_sync: waits for `stream`, then raises ScratchtapeError if a grouped f16 GEMM's bounded slot wait gave up
+    since the last check (its outputs are not valid)."""
+    _lib.call("st_sync", _stream(stream))
+
+
+def set_wait_limit(polls: int) -> None:
+    """st_set_wait_limit: polls before a slot wait of the grouped f16 kernel gives up (negative: the default)."""
+    _lib.call("st_set_wait_limit", int(polls))
