@@ -134,8 +134,9 @@ st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_stream strea
  * split-k partials live in a fixed per-device array of
  * ST_NOALLOC_SCRATCH_BYTES instead of the library's arena, and the call
  * allocates and frees nothing.  A group whose partials need more is refused
- * with ST_ERR_INVALID.  Every call on a device shares that device's array:
- * calls that overlap on one device race. */
+ * with ST_ERR_INVALID before anything is launched (no output is touched).
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device race. */
 st_status st_matmul_grouped_noalloc(const st_gemm *gemms, int64_t count, st_stream stream);
 
 /* gpu_step/matmul.rs:97-102 `f16_enabled`: 1 unless the environment sets

@@ -2,9 +2,16 @@
 //! signatures (`src/gpu_step/matmul.rs:86-106`, `src/tensor.rs:241`, `src/gpu_step/rows.rs:65, 90`,
 //! `src/gpu_step/knn/ivf.rs:466`).
 //!
-//! - Device buffers name their address through [`DeviceBuffer`]; the runtime's buffer handle
-//!   implements it (the role of `cubecl::server::Handle` in `src/gpu_step/mod.rs:139-151`).
-//!   [`DevicePtr`] wraps a bare device address.
+//! - Device buffers name their address and byte length through [`DeviceBuffer`], an `unsafe`
+//!   trait: an implementor promises that the range is device memory that stays valid while the
+//!   work enqueued on it runs. The runtime's buffer handle implements it (the role of
+//!   `cubecl::server::Handle` in `src/gpu_step/mod.rs:139-151`); [`DevicePtr`] wraps a bare
+//!   address and length, and building one is `unsafe` for the same reason.
+//! - Every safe wrapper checks, before the call, that each buffer holds every element the call
+//!   reads or writes for the shapes given (and panics, as the reference's asserts do, if one does
+//!   not), so a safe call never reaches outside its buffers. Calls whose extents depend on data in
+//!   device memory (the cell table of [`knn_search_ivf_2bit`]), or that free or share memory
+//!   behind the caller's back ([`scratch_release`], [`matmul_grouped_noalloc`]), are `unsafe fn`.
 //! - Every call goes on the calling thread's stream, [`stream`] (the default stream unless
 //!   [`set_stream`] chose another), as the reference puts every launch on its one queue.
 //! - A failed status panics with the library's message, as the reference's asserts do.
@@ -15,18 +22,38 @@ pub use crate::check;
 use crate as sys;
 use crate::st_stream;
 
-/// Device memory that can name its device address.
-pub trait DeviceBuffer {
+/// Device memory that can name its device address and length.
+///
+/// # Safety
+/// `device_ptr() .. device_ptr() + byte_len()` must be device memory of the current device that
+/// stays allocated, and is not used by anything else the call does not know of, until the work
+/// enqueued on it has finished.
+pub unsafe trait DeviceBuffer {
     fn device_ptr(&self) -> *mut c_void;
+    fn byte_len(&self) -> usize;
 }
 
-/// A bare device address (a `hipMalloc` result, or a torch tensor's `data_ptr()`).
+/// A bare device range (a `hipMalloc` result, or a torch tensor's `data_ptr()` and byte size).
 #[derive(Clone, Copy, Debug)]
-pub struct DevicePtr(pub *mut c_void);
+pub struct DevicePtr {
+    ptr: *mut c_void,
+    bytes: usize,
+}
 
-impl DeviceBuffer for DevicePtr {
+impl DevicePtr {
+    /// # Safety
+    /// `ptr .. ptr + bytes` must be device memory meeting [`DeviceBuffer`]'s contract.
+    pub unsafe fn new(ptr: *mut c_void, bytes: usize) -> Self {
+        Self { ptr, bytes }
+    }
+}
+
+unsafe impl DeviceBuffer for DevicePtr {
     fn device_ptr(&self) -> *mut c_void {
-        self.0
+        self.ptr
+    }
+    fn byte_len(&self) -> usize {
+        self.bytes
     }
 }
 
@@ -43,6 +70,24 @@ pub fn dptr<T, H: DeviceBuffer + ?Sized>(h: &H) -> *mut T {
 /// A buffer's device address as a read-only element pointer.
 pub fn ptr<T, H: DeviceBuffer + ?Sized>(h: &H) -> *const T {
     h.device_ptr() as *const T
+}
+
+/// Panics unless `h` holds `count` elements of `T` (`count` counts from the buffer's start).
+fn need<T, H: DeviceBuffer + ?Sized>(h: &H, count: usize, what: &str) {
+    let bytes = count.checked_mul(std::mem::size_of::<T>());
+    match bytes {
+        Some(b) if b <= h.byte_len() => {}
+        _ => panic!("{}: the buffer holds {} bytes, the call reaches {} elements of {} bytes", what,
+                    h.byte_len(), count, std::mem::size_of::<T>()),
+    }
+}
+
+fn mul(a: usize, b: usize) -> usize {
+    a.checked_mul(b).expect("extent overflows usize")
+}
+
+fn add(a: usize, b: usize) -> usize {
+    a.checked_add(b).expect("extent overflows usize")
 }
 
 thread_local! {
@@ -90,6 +135,21 @@ impl<'a, H: DeviceBuffer + ?Sized> MatRef<'a, H> {
     /// b·t .. b·t + t, columns col0 + h·width .. + width, of a row-major [B·t, cols] buffer.
     pub fn heads(h: &'a H, col0: usize, cols: usize, t: usize, heads: usize, width: usize) -> Self {
         Self { off: col0, stride: t * cols, ld: cols, group: heads, inner: width, ..Self::new(h) }
+    }
+
+    /// One past the last element of `h` that `batch` logical [rows, cols] matrices reach.
+    pub fn end(&self, batch: usize, rows: usize, cols: usize) -> usize {
+        if batch == 0 || rows == 0 || cols == 0 {
+            return self.off;
+        }
+        let (sr, sc) = if self.trans { (cols, rows) } else { (rows, cols) };
+        let ld = if self.ld == 0 { sc } else { self.ld };
+        let group = self.group.max(1);
+        let mut zmax = 0usize;
+        for z in 0..batch {
+            zmax = zmax.max(add(mul(z / group, self.stride), mul(z % group, self.inner)));
+        }
+        add(add(self.off, zmax), add(mul(sr - 1, ld), sc))
     }
 
     pub fn raw(&self) -> sys::st_matref {
@@ -168,6 +228,39 @@ impl<'a, H: DeviceBuffer + ?Sized> Epilogue<'a, H> {
     }
 }
 
+/// Panics unless every buffer of a GEMM holds what the call reads and writes: a [m, k], b [k, n]
+/// and out [m, n] per batch matrix through their `MatRef`s, bias `bias_stride`·z + n per matrix,
+/// mask and residual laid out as out, and the column sums at off + z·stride + n of out's buffer.
+fn check_gemm<H: DeviceBuffer + ?Sized>(
+    a: &MatRef<'_, H>,
+    b: &MatRef<'_, H>,
+    out: &MatRef<'_, H>,
+    batch: usize,
+    m: usize,
+    k: usize,
+    n: usize,
+    epi: &Epilogue<'_, H>,
+) {
+    if batch == 0 || m == 0 || n == 0 {
+        return;
+    }
+    need::<f32, H>(a.h, a.end(batch, m, k), "matmul a");
+    need::<f32, H>(b.h, b.end(batch, k, n), "matmul b");
+    let out_end = out.end(batch, m, n);
+    need::<f32, H>(out.h, out_end, "matmul out");
+    if let Some((h, off)) = epi.bias {
+        need::<f32, H>(h, add(off, add(mul(batch - 1, epi.bias_stride), n)), "matmul bias");
+    }
+    for (o, what) in [(epi.mask, "matmul mask"), (epi.residual, "matmul residual")] {
+        if let Some((h, off)) = o {
+            need::<f32, H>(h, add(off, out_end - out.off), what);
+        }
+    }
+    if let Some((off, stride)) = epi.col_sum {
+        need::<f32, H>(out.h, add(off, add(mul(batch - 1, stride), n)), "matmul col_sum");
+    }
+}
+
 /// `matmul` (`src/gpu_step/matmul.rs:86`): out[z] (+)= epilogue(a[z] @ b[z]) for z in 0..batch, a[z]
 /// logically [m, k], b[z] [k, n], out[z] row-major [m, n]; the f16 route when [`f16_enabled`].
 pub fn matmul<H: DeviceBuffer + ?Sized>(
@@ -180,6 +273,7 @@ pub fn matmul<H: DeviceBuffer + ?Sized>(
     n: usize,
     epi: Epilogue<'_, H>,
 ) {
+    check_gemm(&a, &b, &out, batch, m, k, n, &epi);
     let (a, b, o, e) = (a.raw(), b.raw(), out.raw(), epi.raw());
     check(unsafe { sys::st_matmul(&a, &b, &o, batch as i64, m as i64, k as i64, n as i64, &e, stream()) });
 }
@@ -195,6 +289,7 @@ pub fn matmul_f32<H: DeviceBuffer + ?Sized>(
     n: usize,
     epi: Epilogue<'_, H>,
 ) {
+    check_gemm(&a, &b, &out, batch, m, k, n, &epi);
     let (a, b, o, e) = (a.raw(), b.raw(), out.raw(), epi.raw());
     check(unsafe { sys::st_matmul_f32(&a, &b, &o, batch as i64, m as i64, k as i64, n as i64, &e, stream()) });
 }
@@ -212,6 +307,7 @@ pub fn matmul_with<H: DeviceBuffer + ?Sized>(
     epi: Epilogue<'_, H>,
     use_f16: bool,
 ) {
+    check_gemm(&a, &b, &out, batch, m, k, n, &epi);
     let (a, b, o, e) = (a.raw(), b.raw(), out.raw(), epi.raw());
     check(unsafe {
         sys::st_matmul_with(&a, &b, &o, batch as i64, m as i64, k as i64, n as i64, &e, use_f16 as i32, stream())
@@ -257,14 +353,24 @@ impl<'a, H: DeviceBuffer + ?Sized> Gemm<'a, H> {
 /// dW and dx, `src/gpu_step/tape.rs:324-347`) as one submission. No GEMM of the group may read or
 /// write memory that another one writes.
 pub fn matmul_grouped<H: DeviceBuffer + ?Sized>(gemms: &[Gemm<'_, H>]) {
+    for g in gemms {
+        check_gemm(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n, &g.epi);
+    }
     let raw: Vec<sys::st_gemm> = gemms.iter().map(|g| g.raw()).collect();
     check(unsafe { sys::st_matmul_grouped(raw.as_ptr(), raw.len() as i64, stream()) });
 }
 
 /// [`matmul_grouped`] without device allocation: split-k partials live in the library's fixed
-/// per-device array (`ST_NOALLOC_SCRATCH_BYTES`); a group needing more panics. Calls that overlap
-/// on one device race on that array.
-pub fn matmul_grouped_noalloc<H: DeviceBuffer + ?Sized>(gemms: &[Gemm<'_, H>]) {
+/// per-device array (`ST_NOALLOC_SCRATCH_BYTES`); a group needing more panics before anything is
+/// launched.
+///
+/// # Safety
+/// Every call on a device shares that device's array: no other call of this function may run on
+/// the same device (on another stream or thread) until this one's work has finished.
+pub unsafe fn matmul_grouped_noalloc<H: DeviceBuffer + ?Sized>(gemms: &[Gemm<'_, H>]) {
+    for g in gemms {
+        check_gemm(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n, &g.epi);
+    }
     let raw: Vec<sys::st_gemm> = gemms.iter().map(|g| g.raw()).collect();
     check(unsafe { sys::st_matmul_grouped_noalloc(raw.as_ptr(), raw.len() as i64, stream()) });
 }
@@ -315,6 +421,12 @@ pub fn layer_norm<H: DeviceBuffer + ?Sized>(
     m: Models,
     out: &LnOut<'_, H>,
 ) {
+    let params_end = add(add(off, mul(m.k.max(1) - 1, m.stride)), mul(2, d));
+    need::<f32, H>(x, mul(rows, d), "layer_norm x");
+    need::<f32, H>(params, params_end, "layer_norm params");
+    need::<f32, H>(out.y, mul(rows, d), "layer_norm y");
+    need::<f32, H>(out.mean, rows, "layer_norm mean");
+    need::<f32, H>(out.rstd, rows, "layer_norm rstd");
     check(unsafe {
         sys::st_layer_norm(
             ptr(x),
@@ -348,6 +460,14 @@ pub fn layer_norm_backward<H: DeviceBuffer + ?Sized>(
     accumulate: bool,
     m: Models,
 ) {
+    let params_end = add(add(off, mul(m.k.max(1) - 1, m.stride)), mul(2, d));
+    for (h, what) in [(dy, "layer_norm_backward dy"), (x, "layer_norm_backward x"), (dx, "layer_norm_backward dx")] {
+        need::<f32, H>(h, mul(rows, d), what);
+    }
+    need::<f32, H>(fwd.mean, rows, "layer_norm_backward mean");
+    need::<f32, H>(fwd.rstd, rows, "layer_norm_backward rstd");
+    need::<f32, H>(params, params_end, "layer_norm_backward params");
+    need::<f32, H>(grads, params_end, "layer_norm_backward grads");
     check(unsafe {
         sys::st_layer_norm_backward(
             ptr(dy),
@@ -371,6 +491,8 @@ pub fn layer_norm_backward<H: DeviceBuffer + ?Sized>(
 /// `softmax` (`src/gpu_step/rows.rs:101-112`): y = softmax(scale · x) per row of x [rows, n]; with
 /// `causal`, row r sees columns 0..=r % t and the rest are 0; `one` is softmax1 (a phantom logit 0).
 pub fn softmax<H: DeviceBuffer + ?Sized>(x: &H, y: &H, rows: usize, n: usize, t: usize, scale: f32, causal: bool, one: bool) {
+    need::<f32, H>(x, mul(rows, n), "softmax x");
+    need::<f32, H>(y, mul(rows, n), "softmax y");
     check(unsafe {
         sys::st_softmax(ptr(x), dptr(y), rows as i64, n as i64, t as i64, scale, causal as i32, one as i32, stream())
     });
@@ -378,6 +500,9 @@ pub fn softmax<H: DeviceBuffer + ?Sized>(x: &H, y: &H, rows: usize, n: usize, t:
 
 /// `softmax_backward` (`src/gpu_step/rows.rs:114-123`): dx = scale · y · (dy - sum(dy · y)).
 pub fn softmax_backward<H: DeviceBuffer + ?Sized>(dy: &H, y: &H, dx: &H, rows: usize, n: usize, scale: f32) {
+    for (h, what) in [(dy, "softmax_backward dy"), (y, "softmax_backward y"), (dx, "softmax_backward dx")] {
+        need::<f32, H>(h, mul(rows, n), what);
+    }
     check(unsafe { sys::st_softmax_backward(ptr(dy), ptr(y), dptr(dx), rows as i64, n as i64, scale, stream()) });
 }
 
@@ -394,6 +519,10 @@ pub fn attention_fused_fwd<H: DeviceBuffer + ?Sized>(
     scale: f32,
     one: bool,
 ) {
+    let ctx_len = mul(mul(mul(b, t), h), hd);
+    need::<f32, H>(qkv, mul(3, ctx_len), "attention qkv");
+    need::<f32, H>(ctx, ctx_len, "attention ctx");
+    need::<f32, H>(lse, mul(mul(b, h), t), "attention lse");
     check(unsafe {
         sys::st_attention_fused_fwd(
             ptr(qkv),
@@ -423,6 +552,12 @@ pub fn attention_fused_bwd<H: DeviceBuffer + ?Sized>(
     hd: usize,
     scale: f32,
 ) {
+    let ctx_len = mul(mul(mul(b, t), h), hd);
+    need::<f32, H>(qkv, mul(3, ctx_len), "attention qkv");
+    need::<f32, H>(dqkv, mul(3, ctx_len), "attention dqkv");
+    need::<f32, H>(ctx, ctx_len, "attention ctx");
+    need::<f32, H>(dctx, ctx_len, "attention dctx");
+    need::<f32, H>(lse, mul(mul(b, h), t), "attention lse");
     check(unsafe {
         sys::st_attention_fused_bwd(
             ptr(qkv),
@@ -442,11 +577,17 @@ pub fn attention_fused_bwd<H: DeviceBuffer + ?Sized>(
 
 /// Quantises f32 keys [n, d] to the store's 2-bit codes and per-key scales.
 pub fn knn_quantize_2bit<H: DeviceBuffer + ?Sized>(keys: &H, n: usize, d: usize, codes: &H, scales: &H) {
+    need::<f32, H>(keys, mul(n, d), "knn_quantize_2bit keys");
+    need::<u8, H>(codes, mul(n, d) / 4, "knn_quantize_2bit codes");
+    need::<f32, H>(scales, n, "knn_quantize_2bit scales");
     check(unsafe { sys::st_knn_quantize_2bit(ptr(keys), n as i64, d as i64, dptr(codes), dptr(scales), stream()) });
 }
 
 /// Per-key squared norms of the dequantised 2-bit keys (what the store file keeps per tile).
 pub fn knn_key_norms_2bit<H: DeviceBuffer + ?Sized>(codes: &H, scales: &H, n: usize, d: usize, norms: &H) {
+    need::<u8, H>(codes, mul(n, d) / 4, "knn_key_norms_2bit codes");
+    need::<f32, H>(scales, n, "knn_key_norms_2bit scales");
+    need::<f32, H>(norms, n, "knn_key_norms_2bit norms");
     check(unsafe { sys::st_knn_key_norms_2bit(ptr(codes), ptr(scales), n as i64, d as i64, dptr(norms), stream()) });
 }
 
@@ -461,6 +602,10 @@ pub fn knn_centroid_digit_bytes(nlist: usize, d: usize) -> usize {
 /// The centroid store of probe selection, built once per index (`Cent::new`,
 /// `src/gpu_step/knn/ivf.rs:62-69`): digit blocks, exponents and norms.
 pub fn knn_centroids_prep<H: DeviceBuffer + ?Sized>(centroids: &H, nlist: usize, d: usize, digits: &H, cexp: &H, cnorm: &H) {
+    need::<f32, H>(centroids, mul(nlist, d), "knn_centroids_prep centroids");
+    need::<u8, H>(digits, knn_centroid_digit_bytes(nlist, d), "knn_centroids_prep digits");
+    need::<i32, H>(cexp, nlist, "knn_centroids_prep cexp");
+    need::<f64, H>(cnorm, nlist, "knn_centroids_prep cnorm");
     check(unsafe {
         sys::st_knn_centroids_prep(ptr(centroids), nlist as i64, d as i64, dptr(digits), dptr(cexp), dptr(cnorm), stream())
     });
@@ -479,6 +624,11 @@ pub fn knn_probe<H: DeviceBuffer + ?Sized>(
     nprobe: usize,
     probes: &H,
 ) {
+    need::<u8, H>(digits, knn_centroid_digit_bytes(nlist, d), "knn_probe digits");
+    need::<i32, H>(cexp, nlist, "knn_probe cexp");
+    need::<f64, H>(cnorm, nlist, "knn_probe cnorm");
+    need::<f32, H>(queries, mul(nq, d), "knn_probe queries");
+    need::<i32, H>(probes, mul(nq, nprobe), "knn_probe probes");
     check(unsafe {
         sys::st_knn_probe(
             ptr(digits),
@@ -497,7 +647,12 @@ pub fn knn_probe<H: DeviceBuffer + ?Sized>(
 
 /// The scored part of `search_ivf` (`src/gpu_step/knn/ivf.rs:466`): each query's top-k keys over
 /// its probed cells, nearest first, as key indices [nq, k] and distances [nq, k].
-pub fn knn_search_ivf_2bit<H: DeviceBuffer + ?Sized>(
+///
+/// # Safety
+/// The kernel reads the rows `cell_start` names, which live in device memory and cannot be
+/// checked here: `cell_start` must be non-decreasing, and `codes` and `scales` must hold
+/// `cell_start[ncells]` keys (`d / 4` bytes and one f32 each). The other buffers are checked.
+pub unsafe fn knn_search_ivf_2bit<H: DeviceBuffer + ?Sized>(
     codes: &H,
     scales: &H,
     cell_start: &H,
@@ -512,6 +667,11 @@ pub fn knn_search_ivf_2bit<H: DeviceBuffer + ?Sized>(
     out_idx: &H,
     out_dist: &H,
 ) {
+    need::<i64, H>(cell_start, add(ncells, 1), "knn_search_ivf_2bit cell_start");
+    need::<f32, H>(queries, mul(nq, d), "knn_search_ivf_2bit queries");
+    need::<i32, H>(probes, mul(nq, nprobe), "knn_search_ivf_2bit probes");
+    need::<i64, H>(out_idx, mul(nq, k), "knn_search_ivf_2bit out_idx");
+    need::<f32, H>(out_dist, mul(nq, k), "knn_search_ivf_2bit out_dist");
     check(unsafe {
         sys::st_knn_search_ivf_2bit(
             ptr(codes),
@@ -547,6 +707,12 @@ pub fn knn_search_masked_2bit<H: DeviceBuffer + ?Sized>(
     out_idx: &H,
     out_dist: &H,
 ) {
+    need::<u8, H>(codes, mul(nkeys, d) / 4, "knn_search_masked_2bit codes");
+    need::<f32, H>(scales, nkeys, "knn_search_masked_2bit scales");
+    need::<f32, H>(queries, mul(nq, d), "knn_search_masked_2bit queries");
+    need::<i64, H>(lohi, mul(nq, 2), "knn_search_masked_2bit lohi");
+    need::<i64, H>(out_idx, mul(nq, k), "knn_search_masked_2bit out_idx");
+    need::<f32, H>(out_dist, mul(nq, k), "knn_search_masked_2bit out_dist");
     check(unsafe {
         sys::st_knn_search_masked_2bit(
             ptr(codes),
@@ -570,8 +736,11 @@ pub fn sync() {
     check(unsafe { sys::st_sync(stream()) });
 }
 
-/// Synchronises and frees the split-k scratch arena; only when no captured graph that used it will
-/// be replayed again.
-pub fn scratch_release() {
+/// Synchronises and frees the library's scratch arenas.
+///
+/// # Safety
+/// No graph that captured a library call may be replayed afterwards (it would use freed memory),
+/// and no other library call may run at the same time (on any thread).
+pub unsafe fn scratch_release() {
     check(unsafe { sys::st_scratch_release() });
 }

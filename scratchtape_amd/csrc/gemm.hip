@@ -481,6 +481,42 @@ st::DmaGemm make_dma(const st_matref *a, const st_matref *b, const st_matref *ou
     return d;
 }
 
+// Split-k of the any-shape kernel, as the reference allows it
+// (matmul.rs:117-123): no epilogue but +=, packed out, and only when the
+// output tiles alone leave CUs idle.  Enough slices to give every CU a
+// workgroup, each keeping at least 4 k-stages.
+void kgemm_splits(const TileCfg &tc, int BK, const st_epilogue &epi, const st_matref *out, int64_t batch, int64_t m,
+                  int64_t k, int64_t n, int64_t &splits, int64_t &slice_k) {
+    const int64_t tiles = batch * cdiv(m, tc.bm) * cdiv(n, tc.bn);
+    const int64_t og = out->group > 0 ? out->group : 1;
+    const bool epi_free = !epi.bias && !epi.relu && !epi.mask && !epi.residual;
+    const bool packed_out = (out->ld == 0 || out->ld == n) && og == 1;
+    splits = 1;
+    const int64_t cus = 256;
+    if (epi_free && packed_out && tiles < cus)
+        splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(cus, tiles), k / (4 * BK)));
+    slice_k = cdiv(cdiv(k, splits), BK) * BK;
+    if (slice_k == 0) slice_k = BK;
+    splits = std::max<int64_t>(1, cdiv(k, slice_k));
+}
+
+// Bytes of split-k scratch gemm_impl would request for these arguments (0
+// when it would request none or refuse them).
+size_t gemm_impl_scratch(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
+                         int64_t k, int64_t n, const st_epilogue &epi, bool use_f16) {
+    if (!a || !b || !out || !a->p || !b->p || !out->p || out->trans || batch <= 0 || m <= 0 || n <= 0 || k <= 0)
+        return 0;
+    const bool f16 = f16_route(use_f16, epi, b, m, k, n);
+    const st::DmaGemm d = make_dma(a, b, out, batch, m, k, n, epi, f16);
+    size_t dma = 0;
+    if ((dma = st::gemm_dma_scratch(d)) || st::gemm_dma_takes(d)) return dma;
+    const TileCfg tc = choose_tile(batch, m, n);
+    int64_t splits = 1, slice_k = 0;
+    kgemm_splits(tc, f16 ? 64 : 32, epi, out, batch, m, k, n, splits, slice_k);
+    if (splits <= 1) return 0;
+    return sizeof(float) * (size_t)(batch * splits * m * n + (epi.has_col_sum ? batch * splits * n : 0));
+}
+
 st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out, int64_t batch, int64_t m,
                     int64_t k, int64_t n, const st_epilogue *epi_in, bool use_f16, hipStream_t stream) {
     st::clear_error();
@@ -507,21 +543,8 @@ st_status gemm_impl(const st_matref *a, const st_matref *b, const st_matref *out
 
     TileCfg tc = choose_tile(batch, m, n);
     const int BK = f16 ? 64 : 32;
-    const int64_t tiles = batch * cdiv(m, tc.bm) * cdiv(n, tc.bn);
-
-    // Split-k as the reference allows it (matmul.rs:117-123): no epilogue but
-    // +=, packed out, and only when the output tiles alone leave CUs idle.
-    // Enough slices to give every CU a workgroup, each keeping at least 4
-    // k-stages.
-    const bool epi_free = !epi.bias && !epi.relu && !epi.mask && !epi.residual;
-    const bool packed_out = (out->ld == 0 || out->ld == n) && og == 1;
-    int64_t splits = 1;
-    const int64_t cus = 256;
-    if (epi_free && packed_out && tiles < cus)
-        splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(cus, tiles), k / (4 * BK)));
-    int64_t slice_k = cdiv(cdiv(k, splits), BK) * BK;
-    if (slice_k == 0) slice_k = BK;
-    splits = std::max<int64_t>(1, cdiv(k, slice_k));
+    int64_t splits = 1, slice_k = 0;
+    kgemm_splits(tc, BK, epi, out, batch, m, k, n, splits, slice_k);
     if (batch * splits > 65535) return st::fail(ST_ERR_INVALID, "batch %lld too large for one launch", (long long)batch);
     if (cdiv(m, tc.bm) > 65535) return st::fail(ST_ERR_INVALID, "m = %lld too large for one launch", (long long)m);
 
@@ -658,6 +681,22 @@ extern "C" st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_s
         const bool use_tall = tall_tiles >= 256;
         for (const st::DmaGemm &d : elig[f]) grp[f + 2 * (use_tall && st::group_tall(d))].push_back(d);
     }
+    // All or nothing: the launches below share the split-k scratch one after
+    // another, so the largest need among them is requested before the first
+    // launch.  A refusal (a fixed scratch too small, an arena that cannot grow
+    // under graph capture or out of memory) then leaves every output as it
+    // was; every later request fits what is already there.
+    size_t need = 0;
+    for (int f = 0; f < 4; f++)
+        for (size_t c = 0; c < grp[f].size(); c += st::GROUP_MAX) {
+            const int cnt = (int)std::min<size_t>(st::GROUP_MAX, grp[f].size() - c);
+            need = std::max(need, st::gemm_group_scratch(grp[f].data() + c, cnt, (f & 1) != 0, (f & 2) != 0));
+        }
+    for (const int64_t i : rest) {
+        const st_gemm &g = gemms[i];
+        need = std::max(need, gemm_impl_scratch(&g.a, &g.b, &g.out, g.batch, g.m, g.k, g.n, g.epi, g.use_f16 != 0));
+    }
+    if (need && !st::scratch(st::SCRATCH_SPLITK, need, s)) return st::scratch_status();
     for (int f = 0; f < 4; f++)
         for (size_t c = 0; c < grp[f].size(); c += st::GROUP_MAX) {
             const int cnt = (int)std::min<size_t>(st::GROUP_MAX, grp[f].size() - c);

@@ -34,6 +34,10 @@ struct DmaGemm {
 // strides).  Returns false, having enqueued nothing, when they do not;
 // otherwise true, with *status the launch status.
 bool gemm_dma(const DmaGemm &g, hipStream_t stream, st_status *status);
+// Whether gemm_dma takes g, and the bytes of split-k scratch it then requests
+// (0 when it does not split).
+bool gemm_dma_takes(const DmaGemm &g);
+size_t gemm_dma_scratch(const DmaGemm &g);
 
 // Grouped launches (gemm_group.hip): at most GROUP_MAX GEMMs of one route
 // (f16 or f32) and one tile shape (group_tall: m % 256 == 0, 256-row tiles;
@@ -44,6 +48,8 @@ constexpr int GROUP_MAX = 16;
 bool group_eligible(const DmaGemm &g);
 bool group_tall(const DmaGemm &g);
 st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream);
+// Bytes of split-k scratch gemm_group requests for the same arguments.
+size_t gemm_group_scratch(const DmaGemm *items, int count, bool f16, bool tall);
 // Reads and clears the current device's count of grouped-kernel slot waits
 // that gave up; ST_ERR_HIP with a message if there were any.  The caller has
 // synchronised the work it wants covered.

@@ -310,11 +310,13 @@ bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-}  // namespace
+// The kernel's tile and split-k for d; false when the kernel does not take d.
+struct DmaPlan {
+    int bm, bn;
+    int64_t splits, slice_k;
+};
 
-namespace st {
-
-bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
+bool dma_plan(const st::DmaGemm &d, DmaPlan &p) {
     const int64_t m = d.m, n = d.n, k = d.k, batch = d.batch;
     if (k <= 0 || k % BK != 0) return false;
     // 16-byte runs everywhere: operands for the DMA, out / mask / residual for
@@ -358,10 +360,34 @@ bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
         }
     }
     if (best < 0) return false;
-    const int bm = cands[best].bm, bn = cands[best].bn;
-    const int64_t slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
-    const int64_t splits = cdiv(k, slice_k);
-    if (batch * splits > 65535 || m / bm > 65535 || n / bn > INT32_MAX) return false;
+    p.bm = cands[best].bm;
+    p.bn = cands[best].bn;
+    p.slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
+    p.splits = cdiv(k, p.slice_k);
+    return !(batch * p.splits > 65535 || m / p.bm > 65535 || n / p.bn > INT32_MAX);
+}
+
+}  // namespace
+
+namespace st {
+
+bool gemm_dma_takes(const DmaGemm &d) {
+    DmaPlan p;
+    return dma_plan(d, p);
+}
+
+size_t gemm_dma_scratch(const DmaGemm &d) {
+    DmaPlan p;
+    if (!dma_plan(d, p) || p.splits <= 1) return 0;
+    return sizeof(float) * (size_t)(d.batch * p.splits * (d.m * d.n + (d.has_cs ? d.n : 0)));
+}
+
+bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
+    DmaPlan plan;
+    if (!dma_plan(d, plan)) return false;
+    const int64_t m = d.m, n = d.n, k = d.k, batch = d.batch;
+    const int bm = plan.bm, bn = plan.bn;
+    const int64_t slice_k = plan.slice_k, splits = plan.splits;
 
     KArgs g;
     std::memset(&g, 0, sizeof g);

@@ -1145,20 +1145,14 @@ void schedule(GroupArgs &ga, int L) {
     last_key = std::move(key);
 }
 
-template <class C>
-st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupArgs), hipStream_t stream) {
+// Split-k where the epilogue allows it, so that no unit holds more k-stages
+// than a CU's fair share of the whole group (nor fewer than 4); TM-row tiles,
+// every slice keeps at least NS - 1 stages.
+void group_splits(const st::DmaGemm *items, int count, int TM, int NS, int cus, std::vector<int64_t> &splits,
+                  std::vector<int64_t> &slice_k) {
     using st::DmaGemm;
-    using st::fail;
-    constexpr int TM = C::TM, NS = C::NS;
-    if (count <= 0) return ST_OK;
-    if (count > st::GROUP_MAX) return fail(ST_ERR_INVALID, "at most %d GEMMs per grouped launch", st::GROUP_MAX);
-    static thread_local int cus_cached = 0;
-    if (!cus_cached) cus_cached = cu_count();
-    const int cus = cus_cached;
-
-    // Split-k where the epilogue allows it, so that no unit holds more
-    // k-stages than a CU's fair share of the whole group (nor fewer than 4).
-    std::vector<int64_t> splits(count, 1), slice_k(count, 0);
+    splits.assign(count, 1);
+    slice_k.assign(count, 0);
     double total = 0;
     for (int i = 0; i < count; i++)
         total += (double)items[i].batch * (items[i].m / TM) * (items[i].n / TN) * (items[i].k / BK);
@@ -1170,7 +1164,6 @@ st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupAr
             while ((double)d.k / BK / sp > fair && d.k / (2 * sp) >= 4 * BK) sp *= 2;
         int64_t sk = cdiv(cdiv(d.k, sp), BK) * BK;
         int64_t n_sp = cdiv(d.k, sk);
-        // Every slice keeps at least NS - 1 stages.
         while (n_sp > 1 && d.k - (n_sp - 1) * sk < (NS - 1) * BK) {
             sp /= 2;
             sk = cdiv(cdiv(d.k, sp), BK) * BK;
@@ -1179,6 +1172,38 @@ st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupAr
         splits[i] = n_sp;
         slice_k[i] = sk;
     }
+}
+
+// Floats of split partials (and their column-sum partials) a grouped launch
+// needs.
+size_t group_part_floats(const st::DmaGemm *items, int count, const std::vector<int64_t> &splits) {
+    size_t f = 0;
+    for (int i = 0; i < count; i++)
+        if (splits[i] > 1) {
+            const st::DmaGemm &d = items[i];
+            f += (size_t)(d.batch * splits[i] * d.m * d.n);
+            if (d.has_cs) f += (size_t)(d.batch * splits[i] * d.n);
+        }
+    return f;
+}
+
+int group_cus() {
+    static thread_local int cus_cached = 0;
+    if (!cus_cached) cus_cached = cu_count();
+    return cus_cached;
+}
+
+template <class C>
+st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupArgs), hipStream_t stream) {
+    using st::DmaGemm;
+    using st::fail;
+    constexpr int TM = C::TM, NS = C::NS;
+    if (count <= 0) return ST_OK;
+    if (count > st::GROUP_MAX) return fail(ST_ERR_INVALID, "at most %d GEMMs per grouped launch", st::GROUP_MAX);
+    const int cus = group_cus();
+
+    std::vector<int64_t> splits, slice_k;
+    group_splits(items, count, TM, NS, cus, splits, slice_k);
     // Longest units first.
     std::vector<int> order(count);
     std::iota(order.begin(), order.end(), 0);
@@ -1315,6 +1340,13 @@ st_status check_group_waits() {
                 "grouped GEMM: %u slot wait(s) gave up after %u polls; the outputs of the grouped f16 GEMMs run "
                 "since the last st_sync are not valid",
                 n, g_wait_polls.load(std::memory_order_relaxed));
+}
+
+size_t gemm_group_scratch(const DmaGemm *items, int count, bool f16, bool tall) {
+    const int TM = tall ? 256 : 128, NS = f16 ? r16::Tall16::NS : (tall ? Tall::NS : Square::NS);
+    std::vector<int64_t> splits, slice_k;
+    group_splits(items, count, TM, NS, group_cus(), splits, slice_k);
+    return sizeof(float) * group_part_floats(items, count, splits);
 }
 
 st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipStream_t stream) {

@@ -16,9 +16,18 @@
 // One wave64 per row (4 rows per 256-thread workgroup); each lane walks the
 // row with stride 64, and the row max / sum are fixed butterfly reductions
 // over the wave, so results are deterministic.  The parameter gradients are
-// column sums in two passes: partial sums over 128-row chunks (4 row lanes
-// per column, combined in a fixed order), then the chunks summed in order.  Contraction is off so that
-// scale*x - m rounds the product first, as the reference's CPU tape does.
+// column sums in two passes, each in a fixed order, on one of two paths:
+//  - scalar path (any d, offset or alignment): k_ln_bwd_part sums 128-row
+//    chunks (4 row lanes per column, combined in a fixed order) and
+//    k_ln_bwd_sum adds the chunks in ascending order;
+//  - vector path (d % 4 == 0 up to 1024, 16-byte aligned rows and parameter
+//    sets): k_ln_bwd4 sums 16-row chunks (each of 4 waves adds its rows in
+//    row order; the 4 waves' sums are added in wave order) and
+//    k_ln_bwd_sum4 adds a column's chunks as 16 slices, each slice's chunks
+//    in ascending order, the 16 slice sums in a fixed tree order.
+// The two paths add in different orders, so their last bits can differ;
+// each is deterministic.  Contraction is off so that scale*x - m rounds the
+// product first, as the reference's CPU tape does.
 #include "common.h"
 #include "lanes.h"
 

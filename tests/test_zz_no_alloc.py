@@ -64,3 +64,28 @@ def test_noalloc_refuses_partials_beyond_its_scratch(dev):
     assert e.value.status == -1 and "fixed scratch" in str(e.value), str(e.value)
     torch.cuda.synchronize()
     assert bool((out == 3.0).all()), "a refused call must launch nothing"
+
+
+def test_noalloc_refusal_launches_no_group(dev):
+    """Two route groups, of which only the second's split-k partials exceed the fixed scratch: an f16 GEMM that
+    accumulates into its output (128-row tiles, the first launch of the call) and the f32 group above (256-row
+    tiles).  The call is refused before its first launch, so the f16 output keeps its values."""
+    big_a, big_b, big_o = (torch.zeros(s, device=dev) for s in ((4096, 128), (128, 4096), (4096, 4096)))
+    a = torch.zeros(256, 131072, device=dev)
+    b = torch.zeros(131072, 1024, device=dev)
+    out = torch.zeros(256 * 1024 + 1024, device=dev)
+    x = torch.ones(128, 256, device=dev)
+    w = torch.ones(256, 128, device=dev)
+    y = torch.full((128, 128), 3.0, device=dev)
+    calls = [(MatRef(x), MatRef(w), MatRef(y), 1, 128, 256, 128, Epilogue(accumulate=True), True),
+             (MatRef(big_a), MatRef(big_b), MatRef(big_o), 1, 4096, 128, 4096, None, False),
+             (MatRef(a), MatRef(b), MatRef(out), 1, 256, 131072, 1024, Epilogue(col_sum=(256 * 1024, 0)), False)]
+    with pytest.raises(st.ScratchtapeError) as e:
+        st.matmul_grouped(calls, noalloc=True)
+    assert e.value.status == -1 and "fixed scratch" in str(e.value), str(e.value)
+    torch.cuda.synchronize()
+    assert bool((y == 3.0).all()), "the f16 group ran before the refusal"
+    # without the oversized GEMM the same call runs: 3 + 256 in every element
+    st.matmul_grouped(calls[:2], noalloc=True)
+    torch.cuda.synchronize()
+    assert bool((y == 259.0).all())
