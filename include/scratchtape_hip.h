@@ -231,7 +231,12 @@ st_status st_knn_key_norms_2bit(const uint8_t *codes, const float *scales, int64
  * padding), out_dist [nq, k] = max(|q^|^2 + dist, 0) (+inf padding).
  * All pointers are device pointers; d == 256; the store holds fewer than
  * 2^32 keys (cell_start[ncells] < 2^32: key indices are 32-bit inside the
- * top-k keys). */
+ * top-k keys).  A batch whose nq * nprobe probes reach ncells or more (each
+ * cell probed once or more on average; the reference groups such batches by
+ * cell, ivf.rs:491-499) is scanned cell-major: each probed cell is read once
+ * for up to four of its queries, with the per-pair lists in the library's
+ * kNN scratch arena (nq * nprobe * 1 KiB; serialise such calls per device,
+ * and run one before capturing a graph).  Smaller batches use no scratch. */
 st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *scales,
                                  const int64_t *cell_start, int64_t ncells, int64_t max_cell,
                                  const float *queries, const int32_t *probes, int64_t nq,
@@ -243,6 +248,13 @@ st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *scales,
  * a query (int16 values X, power-of-two scale 2^e per vector, e = exponent of
  * max|x| - 14); dd = cnorm - ldexp(sum Q C, qe + ce + 1) in float64 with the
  * integer dot exact; cells ranked by (dd, cell id).  d == 256. */
+
+/* No reference counterpart; for tests and benchmarks.  How
+ * st_knn_search_ivf_2bit scans, process-wide, for calls enqueued afterwards:
+ * 0 (default) chooses by batch size, 1 one workgroup per query (each probed
+ * cell read once per query that probes it), 2 each probed cell read once for
+ * up to four of the queries that probe it.  Both give identical results. */
+st_status st_knn_set_scan_order(int32_t order);
 
 /* Bytes of the digit store st_knn_centroids_prep writes for nlist centroids
  * (4096 per block of 8), or -1 for a width other than 256. */

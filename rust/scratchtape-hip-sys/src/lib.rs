@@ -296,6 +296,7 @@ extern "C" {
         stream: st_stream,
     ) -> st_status;
     /// `search_tagged` / `search_tail` (`src/gpu_step/knn.rs:292-331`) over the quantised store.
+    pub fn st_knn_set_scan_order(order: i32) -> st_status;
     pub fn st_knn_search_masked_2bit(
         codes: *const u8,
         scales: *const f32,

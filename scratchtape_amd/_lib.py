@@ -70,6 +70,7 @@ SIGNATURES = {
     "st_knn_quantize_2bit": [_vp, _i64, _i64, _vp, _vp, _vp],
     "st_knn_search_ivf_2bit": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_key_norms_2bit": [_vp, _vp, _i64, _i64, _vp, _vp],
+    "st_knn_set_scan_order": [_i32],
     "st_knn_search_masked_2bit": [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_store_2bit": [_u64, _i64, _i64, _i64, _vp, _vp, _vp],
     "st_knn_synth_keys_f32": [_u64, _i64, _i64, _i64, _vp, _vp],

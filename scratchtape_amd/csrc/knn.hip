@@ -41,6 +41,7 @@
 // other queries of the batch also probe first, so that their second reads hit
 // the MALL, bought nothing: on this device a MALL-resident buffer reads no
 // faster than a stream from HBM.)
+#include <algorithm>
 #include <cstring>
 #include <type_traits>
 
@@ -410,9 +411,10 @@ struct Kept {
 // kept ones (wl[0, na), sorted): the new keys are sorted in registers, the
 // minimum of each kept key and the mirrored new key (a bitonic split) holds
 // the 128 smallest of both, and a bitonic merge sorts them into wl[0, KMAX).
-// The E8-th smallest goes to *e8 (when there are E8).  Not inlined: it runs a
+// The E8R-th smallest goes to *e8 (when there are E8R).  Not inlined: it runs a
 // few times per wave and query, and inlined its registers would spill the
 // scan loop's.
+template <int E8R>
 __device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, int nb, lds_u64 *e8, int lane) {
     uint64_t nk[2], kp[2];
 #pragma unroll
@@ -427,7 +429,7 @@ __device__ __attribute__((noinline)) Kept merge_new_keys(lds_u64 *wl, int na, in
     bitonic_stage<2, 128, 64>(kp, lane);
     wl[lane] = kp[0];
     wl[64 + lane] = kp[1];
-    if (lane == E8 - 1 && kp[0] != NONE) *e8 = kp[0];
+    if (lane == E8R - 1 && kp[0] != NONE) *e8 = kp[0];
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
     Kept k;
@@ -601,7 +603,7 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     };
     auto wave_compact = [&]() {
         if (nb > 0) {
-            const Kept k = merge_new_keys((lds_u64 *)wl, na, nb, (lds_u64 *)(s_e8 + wave), lane);
+            const Kept k = merge_new_keys<E8>((lds_u64 *)wl, na, nb, (lds_u64 *)(s_e8 + wave), lane);
             na = k.na;
             nb = 0;
             tau_w = k.tau;
@@ -707,7 +709,393 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
     }
 }
 
+// ---------------------------------------------------------------- cell-major search
+//
+// For batches whose queries probe the same cells several times over (the
+// reference batches 2048-16384 queries per call and groups them by cell,
+// ivf.rs:491-499, 528-686), each probed cell is read once for up to QG
+// queries that probe it: one FP8 x FP4 MFMA already scores four query slots
+// (build_aq / score_chunk), so the other three come free.
+//   k_cells_group   (one workgroup) groups the (query, probe) pairs by cell
+//                   into units of at most QG queries of one cell;
+//   k_search_cells  (persistent workgroups taking units from a counter) scans
+//                   a unit's cell once, keeps each slot's exact top-KMAX of the
+//                   cell as k_search keeps a query's, and writes it sorted to
+//                   the pair's list parts[q nprobe + probe];
+//   k_merge_parts   (one wave per query) merges the query's lists, keeping the
+//                   KMAX smallest (bitonic split + merge per list), and writes
+//                   k_search's outputs.
+// The top-KMAX of the union of a query's cells lies in the union of the
+// cells' top-KMAX, and every key is scored as k_search scores it, so the
+// results are k_search's bit for bit.  Which queries share a unit depends on
+// the order of atomics; the results do not.
+
+constexpr int QG = 4;  // query slots per unit
+
+struct CellUnit {
+    int32_t cell, n;   // the cell and its query slots in use (1 .. QG)
+    int32_t qp[QG];    // query * nprobe + probe slot of each
+};
+
+// A probe slot the scan covers: a cell id in [0, ncells), not repeated by an
+// earlier slot of the same query (k_search scans such a cell once as well).
+__device__ __forceinline__ bool probe_used(const int32_t *__restrict__ probes, int64_t q, int j, int32_t nprobe,
+                                           int64_t ncells, int32_t &c) {
+    c = probes[q * nprobe + j];
+    if (c < 0 || c >= ncells) return false;
+    for (int i = 0; i < j; i++)
+        if (probes[q * nprobe + i] == c) return false;
+    return true;
+}
+
+// grid: 1 workgroup of GT threads.  cnt, fill, ubase: ncells ints each;
+// hdr[0] = units written, hdr[1] = the scan's unit counter (set to 0 here);
+// qtau [nq]: each query's pruning bound, set to NONE here.
+constexpr int GT = 1024;
+__global__ __launch_bounds__(GT) void k_cells_group(const int32_t *__restrict__ probes, int32_t nq, int32_t nprobe,
+                                                    int64_t ncells, int32_t *cnt, int32_t *fill, int32_t *ubase,
+                                                    CellUnit *units, int32_t *hdr, uint64_t *qtau) {
+    __shared__ int32_t s[GT];
+    const int tid = threadIdx.x;
+    for (int64_t c = tid; c < ncells; c += GT) {
+        cnt[c] = 0;
+        fill[c] = 0;
+    }
+    for (int64_t q = tid; q < nq; q += GT) qtau[q] = NONE;
+    __syncthreads();
+    const int64_t npairs = (int64_t)nq * nprobe;
+    for (int64_t i = tid; i < npairs; i += GT) {
+        int32_t c;
+        if (probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c)) atomicAdd(&cnt[c], 1);
+    }
+    __syncthreads();
+    // Units per cell (ceil(cnt / QG)), exclusive prefix over the cells: each
+    // thread a contiguous range of cells, the ranges' sums scanned in LDS.
+    const int64_t per = (ncells + GT - 1) / GT;
+    const int64_t c0 = min(ncells, (int64_t)tid * per), c1 = min(ncells, c0 + per);
+    int32_t local = 0;
+    for (int64_t c = c0; c < c1; c++) local += (cnt[c] + QG - 1) / QG;
+    s[tid] = local;
+    __syncthreads();
+    for (int o = 1; o < GT; o <<= 1) {
+        const int32_t v = tid >= o ? s[tid - o] : 0;
+        __syncthreads();
+        s[tid] += v;
+        __syncthreads();
+    }
+    int32_t run = s[tid] - local;
+    for (int64_t c = c0; c < c1; c++) {
+        ubase[c] = run;
+        run += (cnt[c] + QG - 1) / QG;
+    }
+    if (tid == GT - 1) {
+        hdr[0] = s[GT - 1];
+        hdr[1] = 0;
+    }
+    __syncthreads();
+    for (int64_t i = tid; i < npairs; i += GT) {
+        int32_t c;
+        if (!probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c)) continue;
+        const int32_t pos = atomicAdd(&fill[c], 1);
+        CellUnit &u = units[ubase[c] + pos / QG];
+        u.qp[pos % QG] = (int32_t)i;
+        if (pos % QG == 0) {
+            u.cell = c;
+            u.n = min(QG, cnt[c] - pos);
+        }
+    }
+}
+
+// Merges the sorted KMAX-list at B into the sorted one at A, keeping the KMAX
+// smallest (sorted) at A: the minimum of each of A's keys and B's mirrored key
+// is a bitonic sequence holding the KMAX smallest of both, which a bitonic
+// merge sorts.
+__device__ __forceinline__ void merge_lists(lds_u64 *A, const lds_u64 *B, int lane) {
+    uint64_t c[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint64_t a = A[r * 64 + lane];
+        const uint64_t b = shfl_xor_u64(B[(1 - r) * 64 + lane], 63, lane);  // B's key 127 - (64 r + lane)
+        c[r] = a < b ? a : b;
+    }
+    bitonic_stage<2, 128, 64>(c, lane);
+    A[lane] = c[0];
+    A[64 + lane] = c[1];
+}
+
+// grid: persistent workgroups of CTH threads taking units from hdr[1] until
+// hdr[0] are done.  parts [nq nprobe][KMAX] keys (ordered dist bits << 32 |
+// row), each pair's list sorted ascending, NONE-padded.  qtau [nq]: a bound on
+// each query's k-th smallest key over all its cells (keys are distinct, so
+// the k-th smallest key of any one of its cells bounds it); every finished
+// (query, cell) list lowers it, and every later unit of the query drops keys
+// at or above it from the start.  A bound read stale is larger, never wrong.
+// Four waves per workgroup, so that two workgroups share a CU and one's
+// set-up and final merges run while the other streams.
+constexpr int CW = 4;                       // waves per cell-major workgroup
+constexpr int CTH = CW * 64;
+constexpr int E8C = (KMAX + CW - 1) / CW;   // each wave's published rank
+__global__ __launch_bounds__(CTH) void k_search_cells(const uint8_t *codes, const float *scales,
+                                                      const int64_t *__restrict__ cell_start, int64_t ncells,
+                                                      const float *__restrict__ queries, int32_t nprobe, int32_t k,
+                                                      const CellUnit *__restrict__ units, int32_t *hdr,
+                                                      uint64_t *qtau, uint64_t *__restrict__ parts) {
+    __shared__ uint64_t cand[QG][CW * CAPW];  // per slot, per-wave candidate lists
+    __shared__ uint64_t s_tau[QG];            // per slot shared threshold (only decreases within a unit)
+    __shared__ uint64_t s_e8[QG][CW];
+    __shared__ int16_t s_Q[QG * D];
+    __shared__ float s_qs[QG];
+    __shared__ int32_t s_sq[QG];
+    __shared__ int32_t s_next, s_unit, s_len;
+    __shared__ int64_t s_r0;
+    __shared__ CellUnit s_u;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = lane >> 4, col = lane & 15;
+    const int32_t n_units = hdr[0];
+    const int64_t nrows = cell_start[ncells];
+    const int32_t c2_base = 9 * D;
+
+    for (;;) {
+        if (tid == 0) s_unit = atomicAdd(&hdr[1], 1);
+        __syncthreads();
+        const int32_t u = s_unit;
+        if (u >= n_units) break;  // uniform over the workgroup
+        if (tid < (int)(sizeof(CellUnit) / 4))
+            reinterpret_cast<int32_t *>(&s_u)[tid] = reinterpret_cast<const int32_t *>(units + u)[tid];
+        __syncthreads();
+        const int n = s_u.n;
+        if (tid == 0) {
+            const int64_t r0 = cell_start[s_u.cell];
+            s_r0 = r0;
+            s_len = (int32_t)(cell_start[s_u.cell + 1] - r0);
+            s_next = 0;
+        }
+        // An absent slot takes nothing (every key compares above 0).
+        if (tid < QG)
+            s_tau[tid] = tid < n ? __hip_atomic_load(&qtau[s_u.qp[tid] / nprobe], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0ull;
+        if (tid < QG * CW) s_e8[tid / CW][tid % CW] = NONE;
+        if (wave < n) {
+            const QInfo qi = quantize_query(queries + (int64_t)(s_u.qp[wave] / nprobe) * D, lane, s_Q + wave * D);
+            if (lane == 0) {
+                s_qs[wave] = qi.qs;
+                s_sq[wave] = qi.sq;
+            }
+        }
+        __syncthreads();
+
+        v8i aq[2];
+        build_aq(s_Q, n, row, col, aq);
+        float qs[QG];
+        int32_t sq[QG];
+#pragma unroll
+        for (int s = 0; s < QG; s++) {
+            qs[s] = s_qs[s < n ? s : 0];
+            sq[s] = s_sq[s < n ? s : 0];
+        }
+        const int64_t r0 = s_r0;
+        const int32_t len = s_len;
+        const int32_t nchunks = (len + 63) / 64;
+
+        // A store of fewer than 64 rows takes the clamped loads (SMALL).
+        auto fetch = [&](auto small, Chunk &ch) {
+            constexpr bool SMALL = decltype(small)::value;
+            int32_t gl = 0;
+            if (lane == 0) gl = atomicAdd(&s_next, 1);
+            const int32_t g = __builtin_amdgcn_readfirstlane(gl);
+            ch.g = g;
+            const bool live = g < nchunks;
+            const int32_t key0 = g * 64;
+            const int32_t nk = live ? min(64, len - key0) : 0;
+            const int64_t row0 = live ? r0 + key0 : r0;
+            const int64_t base = SMALL ? 0 : (row0 < nrows - 64 ? row0 : nrows - 64);
+            ch.base = base;
+            ch.lo = (int32_t)(row0 - base);
+            ch.hi = ch.lo + nk;
+            load_chunk<SMALL>(codes, scales, base, nrows, row, col, lane, ch);
+        };
+
+        int na[QG], nb[QG];
+        uint64_t tau_w[QG];
+#pragma unroll
+        for (int s = 0; s < QG; s++) {
+            na[s] = 0;
+            nb[s] = 0;
+            tau_w[s] = NONE;
+            uint64_t *wl = cand[s] + wave * CAPW;
+            wl[lane] = NONE;
+            wl[64 + lane] = NONE;
+        }
+        auto refresh = [&](int s) {
+            const uint64_t m = wave_max_u64(lane < CW ? s_e8[s][lane] : 0ull);
+            const uint64_t t = tau_w[s] < m ? tau_w[s] : m;
+            if (lane == 0) atomicMin(reinterpret_cast<unsigned long long *>(&s_tau[s]), (unsigned long long)t);
+            const uint64_t ts = __hip_atomic_load(&s_tau[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const uint64_t cut = t < ts ? t : ts;
+            const uint64_t *wl = cand[s] + wave * CAPW;
+            int c = 0;
+            for (int i = 0; i < na[s]; i += 64) c += __popcll(__ballot(i + lane < na[s] && wl[i + lane] <= cut));
+            na[s] = c;
+        };
+        auto compact = [&](int s) {
+            if (nb[s] > 0) {
+                const Kept kk = merge_new_keys<E8C>((lds_u64 *)(cand[s] + wave * CAPW), na[s], nb[s],
+                                                    (lds_u64 *)(&s_e8[s][wave]), lane);
+                na[s] = kk.na;
+                nb[s] = 0;
+                tau_w[s] = kk.tau;
+            }
+            refresh(s);
+        };
+        auto score = [&](const Chunk &ch, bool merge) {
+            int32_t dq[4], n12;
+            score_chunk(ch, aq, dq, n12);
+            const float sc = ch.sc;
+            const int32_t c2 = c2_base - 8 * n12;
+            const float t1 = (sc * sc) * 0.25f * (float)c2;
+            const uint32_t kidx = (uint32_t)(ch.base + lane);
+            const bool in = lane >= ch.lo && lane < ch.hi;
+#pragma unroll
+            for (int s = 0; s < QG; s++) {
+                if (s >= n) break;  // uniform
+                const int32_t dot = 2 * dq[s] - 3 * sq[s];
+                const float t3 = (sc * qs[s]) * (float)dot;
+                const float dist = t1 - t3 + 0.0f;
+                const uint64_t k64 = ((uint64_t)fkey(dist) << 32) | (uint64_t)kidx;
+                const uint64_t ts = __hip_atomic_load(&s_tau[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const uint64_t tau = tau_w[s] < ts ? tau_w[s] : ts;
+                const bool take = in && k64 < tau;
+                const uint64_t mask = __ballot(take);
+                if (take) {
+                    const int pos = nb[s] + (int)__builtin_amdgcn_mbcnt_hi(
+                                                (uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+                    cand[s][wave * CAPW + KMAX + pos] = k64;
+                }
+                nb[s] += __popcll(mask);
+                if (merge && nb[s] > 64) compact(s);  // at most 128 new keys
+            }
+        };
+
+        // As k_search's scan: each wave's first two chunks kept (below the
+        // query's bound), a compaction and one barrier, then NF chunks in
+        // flight per trip.
+        auto scan = [&](auto small) {
+            Chunk x[NF];
+#pragma unroll
+            for (int i = 0; i < NF; i++) fetch(small, x[i]);
+            asm volatile("" ::: "memory");
+            score(x[0], false);
+            score(x[1], false);
+#pragma unroll
+            for (int s = 0; s < QG; s++)
+                if (s < n) compact(s);
+            fetch(small, x[0]);
+            fetch(small, x[1]);
+            asm volatile("" ::: "memory");
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < QG; s++)
+                if (s < n) refresh(s);
+            while (x[2].g < nchunks) {
+#pragma unroll
+                for (int i = 0; i < NF; i++) {
+                    score(x[(i + 2) % NF], true);
+                    fetch(small, x[(i + 2) % NF]);
+                    asm volatile("" ::: "memory");
+                }
+            }
+        };
+        if (nchunks > 0) {  // uniform
+            if (nrows < 64)
+                scan(std::integral_constant<bool, true>());
+            else
+                scan(std::integral_constant<bool, false>());
+        }
+        // Each wave's kept list of each slot, sorted and NONE-padded to KMAX;
+        // then per slot a merge tree over the waves (wave w takes w + 1, then
+        // w + 2), and the slot's list goes to its pair's part; its k-th key
+        // lowers the query's bound.
+#pragma unroll
+        for (int s = 0; s < QG; s++) {
+            if (s >= n) break;
+            compact(s);
+            uint64_t *wl = cand[s] + wave * CAPW;
+            const uint64_t a0 = lane < na[s] ? wl[lane] : NONE, a1 = 64 + lane < na[s] ? wl[64 + lane] : NONE;
+            wl[lane] = a0;
+            wl[64 + lane] = a1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int step = 1; step < CW; step <<= 1) {
+            if ((wave & (2 * step - 1)) == 0)
+                for (int s = 0; s < n; s++)
+                    merge_lists((lds_u64 *)(cand[s] + wave * CAPW), (const lds_u64 *)(cand[s] + (wave + step) * CAPW),
+                                lane);
+            __syncthreads();
+        }
+        for (int i = tid; i < n * KMAX; i += CTH) {
+            const int s = i / KMAX, e = i % KMAX;
+            parts[(int64_t)s_u.qp[s] * KMAX + e] = cand[s][e];
+        }
+        if (tid < n) {
+            const uint64_t kth = cand[tid][k - 1];
+            if (kth != NONE)
+                __hip_atomic_fetch_min(&qtau[s_u.qp[tid] / nprobe], kth, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();  // LDS is reused by the next unit
+    }
+}
+
+// grid: one 64-thread workgroup per query.  Merges the query's per-probe
+// lists (the slots k_cells_group used; others are skipped) and writes
+// k_search's outputs: ranks 0 .. k - 1, max(|Q qs|^2 + dist, 0), -1 / +inf
+// padding.
+__global__ __launch_bounds__(64) void k_merge_parts(const uint64_t *__restrict__ parts,
+                                                    const int32_t *__restrict__ probes, int32_t nprobe,
+                                                    int64_t ncells, const float *__restrict__ queries, int32_t k,
+                                                    int64_t *__restrict__ out_idx, float *__restrict__ out_dist) {
+    __shared__ int16_t sQ[D];
+    __shared__ uint64_t acc[KMAX], lst[KMAX];
+    const int lane = threadIdx.x;
+    const int64_t q = blockIdx.x;
+    const QInfo qi = quantize_query(queries + q * D, lane, sQ);
+    acc[lane] = NONE;
+    acc[64 + lane] = NONE;
+    for (int j = 0; j < nprobe; j++) {
+        int32_t c;
+        if (!probe_used(probes, q, j, nprobe, ncells, c)) continue;  // uniform
+        const uint64_t *L = parts + (q * nprobe + j) * KMAX;
+        lst[lane] = L[lane];
+        lst[64 + lane] = L[64 + lane];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        merge_lists((lds_u64 *)acc, (const lds_u64 *)lst, lane);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int rank = r * 64 + lane;
+        if (rank >= k) continue;
+        const uint64_t e = acc[rank];
+        if (e != NONE) {
+            const float v = qi.qn + unfkey((uint32_t)(e >> 32));
+            out_idx[q * k + rank] = (int64_t)(uint32_t)e;
+            out_dist[q * k + rank] = v > 0.f ? v : 0.f;
+        } else {
+            out_idx[q * k + rank] = -1;
+            out_dist[q * k + rank] = __builtin_inff();
+        }
+    }
+}
+
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Scan order of st_knn_search_ivf_2bit (st_knn_set_scan_order): 0 chooses,
+// 1 query-major (k_search), 2 cell-major.
+int32_t g_scan_order = 0;
 
 }  // namespace
 
@@ -789,10 +1177,59 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     if (nq > INT32_MAX / PROBE_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many queries for one call");
     if (!st::device_ok()) return ST_ERR_NO_DEVICE;
     const hipStream_t s = st::stream_of(stream);
-    hipLaunchKernelGGL(k_search<false>, dim3((unsigned)nq), dim3(STH), 0, s, codes, scales, cell_start, ncells, queries,
-                       probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist, nullptr, (int64_t)0,
-                       (int64_t)0);
+    // Query-major (a workgroup per query, each probed cell read once per
+    // query that probes it) unless the batch probes the cells over once on
+    // average: then cell-major, each probed cell read once for up to QG
+    // queries.
+    const int64_t npairs = nq * nprobe;
+    const bool cells = g_scan_order == 2 || (g_scan_order == 0 && npairs >= ncells);
+    if (!cells) {
+        hipLaunchKernelGGL(k_search<false>, dim3((unsigned)nq), dim3(STH), 0, s, codes, scales, cell_start, ncells,
+                           queries, probes, (int32_t)nq, (int32_t)nprobe, (int32_t)k, out_idx, out_dist, nullptr,
+                           (int64_t)0, (int64_t)0);
+        ST_LAUNCH_CHECK();
+        return ST_OK;
+    }
+    if (ncells > INT32_MAX) return st::fail(ST_ERR_INVALID, "search_ivf: too many cells for the cell-major scan");
+    // Scratch: per-cell counts, fill counters and unit offsets, the unit
+    // header, the units (at most one per pair) and one KMAX list per pair.
+    const size_t cells_b = (size_t)(3 * ncells + 2) * sizeof(int32_t);
+    const size_t qtau_off = (cells_b + 15) & ~(size_t)15;
+    const size_t units_off = qtau_off + (size_t)nq * sizeof(uint64_t);
+    const size_t parts_off = (units_off + (size_t)npairs * sizeof(CellUnit) + 255) & ~(size_t)255;
+    const size_t bytes = parts_off + (size_t)npairs * KMAX * sizeof(uint64_t);
+    char *base = static_cast<char *>(st::scratch(st::SCRATCH_KNN, bytes, s));
+    if (!base) return st::scratch_status();
+    int32_t *cnt = reinterpret_cast<int32_t *>(base), *fill = cnt + ncells, *ubase = fill + ncells,
+            *hdr = ubase + ncells;
+    uint64_t *qtau = reinterpret_cast<uint64_t *>(base + qtau_off);
+    CellUnit *units = reinterpret_cast<CellUnit *>(base + units_off);
+    uint64_t *parts = reinterpret_cast<uint64_t *>(base + parts_off);
+    hipLaunchKernelGGL(k_cells_group, dim3(1), dim3(GT), 0, s, probes, (int32_t)nq, (int32_t)nprobe, ncells, cnt, fill,
+                       ubase, units, hdr, qtau);
     ST_LAUNCH_CHECK();
+    static thread_local int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    // Persistent workgroups, two per CU (those that find no unit left exit).
+    const unsigned wgs = (unsigned)std::min<int64_t>(npairs, 2 * (int64_t)cus);
+    hipLaunchKernelGGL(k_search_cells, dim3(wgs), dim3(CTH), 0, s, codes, scales, cell_start, ncells, queries,
+                       (int32_t)nprobe, (int32_t)k, units, hdr, qtau, parts);
+    ST_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_merge_parts, dim3((unsigned)nq), dim3(64), 0, s, parts, probes, (int32_t)nprobe, ncells,
+                       queries, (int32_t)k, out_idx, out_dist);
+    ST_LAUNCH_CHECK();
+    return ST_OK;
+}
+
+extern "C" st_status st_knn_set_scan_order(int32_t order) {
+    st::clear_error();
+    if (order < 0 || order > 2) return st::fail(ST_ERR_INVALID, "scan order must be 0, 1 or 2 (got %d)", order);
+    g_scan_order = order;
     return ST_OK;
 }
 

@@ -61,6 +61,12 @@ def synth_keys_f32(seed: int, row0: int, n: int, d: int = 256, device="cuda", st
     return keys
 
 
+def set_scan_order(order: int) -> None:
+    """st_knn_set_scan_order: how search_ivf scans, process-wide (0 chooses by batch size, 1 a workgroup per query,
+    2 each probed cell once for up to four queries)."""
+    _lib.call("st_knn_set_scan_order", int(order))
+
+
 class Centroids:
     """The IVF centroids on the device, quantised for probe selection (ivf.rs:54-69 `Cent`).
 

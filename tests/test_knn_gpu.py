@@ -39,6 +39,15 @@ def test_synthetic_store_is_the_quantised_synthetic_keys(dev):
     np.testing.assert_array_equal(scales.cpu().numpy(), ws)
 
 
+@pytest.fixture(params=[1, 2], ids=["query_major", "cell_major"])
+def scan_order(request):
+    """Runs a search test with each scan order of st_knn_search_ivf_2bit (one workgroup per query; each probed cell
+    read once for up to four queries): both must give the oracle's results."""
+    knn.set_scan_order(request.param)
+    yield request.param
+    knn.set_scan_order(0)
+
+
 def make_store(dev, sizes, seed):
     cell_start = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
     keys = np.random.default_rng(seed).standard_normal((int(cell_start[-1]), D)).astype(np.float32)
@@ -54,6 +63,7 @@ def check_search(dev, store, codes, scales, cell_start, queries, probes, k):
     return widx
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_small_with_edge_cases(dev):
     rng = np.random.default_rng(2)
     ncells = 40
@@ -74,6 +84,7 @@ def test_search_small_with_edge_cases(dev):
     assert sorted(idx[2][:3]) == [0 + sizes[0], 1 + sizes[0], 2 + sizes[0]] and np.all(idx[2][3:] == -1)
 
 
+@pytest.mark.usefixtures("scan_order")
 @pytest.mark.parametrize("sizes", [[1], [0, 37], [20, 0, 43], [64], [30, 35], [1, 128, 1], [64, 64, 2]])
 def test_search_stores_near_one_chunk(dev, sizes):
     # Stores of fewer than 64 keys are read key by key; from 64 keys on, a
@@ -89,6 +100,7 @@ def test_search_stores_near_one_chunk(dev, sizes):
         check_search(dev, store, codes, scales, cs, queries, probes, k)
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_many_cells_and_sixteen_probes(dev):
     # 20000 cells of 0..4 keys, 16 probes (the most a query may have), one repeated.
     rng = np.random.default_rng(21)
@@ -103,6 +115,7 @@ def test_search_many_cells_and_sixteen_probes(dev):
         check_search(dev, store, codes, scales, cs, queries, probes, k)
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_skips_probe_ids_outside_the_cells(dev):
     # A probe id < 0 or >= ncells is skipped (the header's contract).  The oracle sees each row with those ids
     # replaced by a repeat of one of its valid ids (a repeated cell is scanned once), or, for a row with none, by
@@ -131,6 +144,7 @@ def test_search_skips_probe_ids_outside_the_cells(dev):
     assert np.all(idx.cpu().numpy()[2] == -1)
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_many_queries_sharing_cells(dev):
     # 600 queries x 8 probes over 100 cells: every cell is probed by ~48 queries.
     rng = np.random.default_rng(31)
@@ -143,6 +157,7 @@ def test_search_many_queries_sharing_cells(dev):
     check_search(dev, store, codes, scales, cs, queries, probes, 128)
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_ties_break_by_key_index(dev):
     # Identical keys give identical scores: the kept ones must be the lowest indices.
     base = np.random.default_rng(4).standard_normal(D).astype(np.float32)
@@ -155,6 +170,7 @@ def test_search_ties_break_by_key_index(dev):
     np.testing.assert_array_equal(idx.cpu().numpy(), np.tile(np.arange(128), (2, 1)))
 
 
+@pytest.mark.usefixtures("scan_order")
 def test_search_cells_of_the_benchmark_size(dev):
     # Cells of ~10.2k keys (125M / 12288), 8 probes per query.
     rng = np.random.default_rng(6)
@@ -201,6 +217,47 @@ def test_full_store_125m_keys(dev):
     cell_of = np.searchsorted(cs, idx, side="right") - 1
     assert np.all(np.any(cell_of[:, :, None] == probes[:, None, :], axis=2))
     del codes, scales, store
+    torch.cuda.empty_cache()
+
+
+def test_full_store_2048_queries_cell_major(dev):
+    """A large batch on the benchmark's store: 2048 queries x 8 probes over 12288 cells (each cell probed 1.3 times
+    on average, so the call takes the cell-major scan by itself); every query's top-128 bit-exact against the oracle
+    over the batch's probed cells, and every query also against the query-major scan."""
+    n, ncells, nq, nprobe, seed = 125_000_000, 12288, 2048, 8, 12
+    rng = np.random.default_rng(seed)
+    sizes = rng.multinomial(n, np.full(ncells, 1.0 / ncells))
+    cs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    codes = torch.empty((n, D // 4), dtype=torch.uint8, device=dev)
+    scales = torch.empty(n, dtype=torch.float32, device=dev)
+    knn.synth_store_2bit(seed, 0, codes, scales)
+    store = knn.KnnStore2bit(codes, scales, cs)
+    queries = rng.standard_normal((nq, D)).astype(np.float32)
+    probes = np.stack([rng.choice(ncells, nprobe, replace=False) for _ in range(nq)]).astype(np.int32)
+    qd, pd = torch.from_numpy(queries).to(dev), torch.from_numpy(probes).to(dev)
+    idx, dist = store.search_ivf(qd, pd, 128)
+    idx, dist = idx.cpu().numpy(), dist.cpu().numpy()
+    knn.set_scan_order(1)
+    try:
+        idx1, dist1 = store.search_ivf(qd, pd, 128)
+    finally:
+        knn.set_scan_order(0)
+    np.testing.assert_array_equal(idx, idx1.cpu().numpy())
+    np.testing.assert_array_equal(dist, dist1.cpu().numpy())
+    # The oracle scores a compact copy of the batch's distinct probed cells with the probes renumbered into it.
+    cells = np.unique(probes)
+    rows = [np.arange(cs[c], cs[c + 1]) for c in cells]
+    sub_cs = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    allrows = np.concatenate(rows)
+    sel = torch.from_numpy(allrows).to(dev)
+    sc, ss = codes[sel].cpu().numpy(), scales[sel].cpu().numpy()
+    del sel
+    sub_probes = np.searchsorted(cells, probes).astype(np.int32)
+    with oracle.threads(16):
+        widx, wdist = oracle.knn_search(sc, ss, sub_cs, queries, sub_probes, 128)
+    np.testing.assert_array_equal(idx, np.where(widx >= 0, allrows[np.maximum(widx, 0)], -1))
+    np.testing.assert_array_equal(dist, wdist)
+    del codes, scales, store, sc, ss
     torch.cuda.empty_cache()
 
 
