@@ -716,8 +716,8 @@ __global__ __launch_bounds__(STH) void k_search(const uint8_t *codes, const floa
 // ivf.rs:491-499, 528-686), each probed cell is read once for up to QG
 // queries that probe it: one FP8 x FP4 MFMA already scores four query slots
 // (build_aq / score_chunk), so the other three come free.
-//   k_cells_group   (one workgroup) groups the (query, probe) pairs by cell
-//                   into units of at most QG queries of one cell;
+//   k_group_*       group the (query, probe) pairs by cell into units of at
+//                   most QG queries of one cell;
 //   k_search_cells  (persistent workgroups taking units from a counter) scans
 //                   a unit's cell once, keeps each slot's exact top-KMAX of the
 //                   cell as k_search keeps a query's, and writes it sorted to
@@ -748,29 +748,36 @@ __device__ __forceinline__ bool probe_used(const int32_t *__restrict__ probes, i
     return true;
 }
 
-// grid: 1 workgroup of GT threads.  cnt, fill, ubase: ncells ints each;
-// hdr[0] = units written, hdr[1] = the scan's unit counter (set to 0 here);
-// qtau [nq]: each query's pruning bound, set to NONE here.
+// Grouping of the (query, probe) pairs by cell, in four launches: cnt, fill
+// (ncells ints each) and the per-query bounds qtau (nq) cleared; the used
+// pairs counted per cell; the units per cell (ceil(cnt / QG)) scanned into
+// ubase, with hdr[0] = units in all and hdr[1] = the scan's unit counter
+// (0); the pairs scattered into their cells' units.
+__global__ __launch_bounds__(256) void k_group_clear(int64_t ncells, int32_t nq, int32_t *cnt, int32_t *fill,
+                                                     uint64_t *qtau) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < ncells) {
+        cnt[i] = 0;
+        fill[i] = 0;
+    }
+    if (i < nq) qtau[i] = NONE;
+}
+
+__global__ __launch_bounds__(256) void k_group_count(const int32_t *__restrict__ probes, int32_t nq, int32_t nprobe,
+                                                     int64_t ncells, int32_t *cnt) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int32_t c;
+    if (i < (int64_t)nq * nprobe && probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c))
+        atomicAdd(&cnt[c], 1);
+}
+
+// grid: 1 workgroup of GT threads, each a contiguous range of cells; the
+// ranges' sums are scanned in LDS.
 constexpr int GT = 1024;
-__global__ __launch_bounds__(GT) void k_cells_group(const int32_t *__restrict__ probes, int32_t nq, int32_t nprobe,
-                                                    int64_t ncells, int32_t *cnt, int32_t *fill, int32_t *ubase,
-                                                    CellUnit *units, int32_t *hdr, uint64_t *qtau) {
+__global__ __launch_bounds__(GT) void k_group_scan(const int32_t *__restrict__ cnt, int64_t ncells,
+                                                   int32_t *__restrict__ ubase, int32_t *hdr) {
     __shared__ int32_t s[GT];
     const int tid = threadIdx.x;
-    for (int64_t c = tid; c < ncells; c += GT) {
-        cnt[c] = 0;
-        fill[c] = 0;
-    }
-    for (int64_t q = tid; q < nq; q += GT) qtau[q] = NONE;
-    __syncthreads();
-    const int64_t npairs = (int64_t)nq * nprobe;
-    for (int64_t i = tid; i < npairs; i += GT) {
-        int32_t c;
-        if (probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c)) atomicAdd(&cnt[c], 1);
-    }
-    __syncthreads();
-    // Units per cell (ceil(cnt / QG)), exclusive prefix over the cells: each
-    // thread a contiguous range of cells, the ranges' sums scanned in LDS.
     const int64_t per = (ncells + GT - 1) / GT;
     const int64_t c0 = min(ncells, (int64_t)tid * per), c1 = min(ncells, c0 + per);
     int32_t local = 0;
@@ -792,17 +799,21 @@ __global__ __launch_bounds__(GT) void k_cells_group(const int32_t *__restrict__ 
         hdr[0] = s[GT - 1];
         hdr[1] = 0;
     }
-    __syncthreads();
-    for (int64_t i = tid; i < npairs; i += GT) {
-        int32_t c;
-        if (!probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c)) continue;
-        const int32_t pos = atomicAdd(&fill[c], 1);
-        CellUnit &u = units[ubase[c] + pos / QG];
-        u.qp[pos % QG] = (int32_t)i;
-        if (pos % QG == 0) {
-            u.cell = c;
-            u.n = min(QG, cnt[c] - pos);
-        }
+}
+
+__global__ __launch_bounds__(256) void k_group_scatter(const int32_t *__restrict__ probes, int32_t nq, int32_t nprobe,
+                                                       int64_t ncells, const int32_t *__restrict__ cnt,
+                                                       int32_t *fill, const int32_t *__restrict__ ubase,
+                                                       CellUnit *units) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int32_t c;
+    if (i >= (int64_t)nq * nprobe || !probe_used(probes, i / nprobe, (int)(i % nprobe), nprobe, ncells, c)) return;
+    const int32_t pos = atomicAdd(&fill[c], 1);
+    CellUnit &u = units[ubase[c] + pos / QG];
+    u.qp[pos % QG] = (int32_t)i;
+    if (pos % QG == 0) {
+        u.cell = c;
+        u.n = min(QG, cnt[c] - pos);
     }
 }
 
@@ -1049,7 +1060,7 @@ __global__ __launch_bounds__(CTH) void k_search_cells(const uint8_t *codes, cons
 }
 
 // grid: one 64-thread workgroup per query.  Merges the query's per-probe
-// lists (the slots k_cells_group used; others are skipped) and writes
+// lists (the slots the grouping used; others are skipped) and writes
 // k_search's outputs: ranks 0 .. k - 1, max(|Q qs|^2 + dist, 0), -1 / +inf
 // padding.
 __global__ __launch_bounds__(64) void k_merge_parts(const uint64_t *__restrict__ parts,
@@ -1205,8 +1216,13 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     uint64_t *qtau = reinterpret_cast<uint64_t *>(base + qtau_off);
     CellUnit *units = reinterpret_cast<CellUnit *>(base + units_off);
     uint64_t *parts = reinterpret_cast<uint64_t *>(base + parts_off);
-    hipLaunchKernelGGL(k_cells_group, dim3(1), dim3(GT), 0, s, probes, (int32_t)nq, (int32_t)nprobe, ncells, cnt, fill,
-                       ubase, units, hdr, qtau);
+    const unsigned pb = (unsigned)cdiv(npairs, 256);
+    hipLaunchKernelGGL(k_group_clear, dim3((unsigned)cdiv(std::max<int64_t>(ncells, nq), 256)), dim3(256), 0, s,
+                       ncells, (int32_t)nq, cnt, fill, qtau);
+    hipLaunchKernelGGL(k_group_count, dim3(pb), dim3(256), 0, s, probes, (int32_t)nq, (int32_t)nprobe, ncells, cnt);
+    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(GT), 0, s, cnt, ncells, ubase, hdr);
+    hipLaunchKernelGGL(k_group_scatter, dim3(pb), dim3(256), 0, s, probes, (int32_t)nq, (int32_t)nprobe, ncells, cnt,
+                       fill, ubase, units);
     ST_LAUNCH_CHECK();
     static thread_local int cus = 0;
     if (!cus) {
