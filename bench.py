@@ -174,37 +174,60 @@ def time_graph(fn, steps, warmup, stream):
 
 # --------------------------------------------------------------------------- GEMM step set
 
-class StepSet:
-    """Buffers and the 15 GEMM calls of one d=256 training step (f32 operands in HBM)."""
+# The epilogues the reference's device tape gives each Linear (gpu_step/tape.rs:180-189, 324-347): the forward adds
+# the bias (+ ReLU on the first FFN layer, + the residual stream after attention and after the FFN); the backward's
+# dW accumulates into the parameter gradients with the bias gradient as column sums of dY.
+TAPE_EPI = {"qkv": (False, False), "out": (False, True), "ffn1": (True, False), "ffn2": (False, True),
+            "head": (False, False)}  # name -> (relu, residual)
 
-    def __init__(self, dev, seed=1):
+
+class StepSet:
+    """Buffers and the 15 GEMM calls of one d=256 training step (f32 operands in HBM).  With `epilogues`, each
+    Linear's weights and bias share one parameter buffer [W, b] and its gradients one [dW, db], and the calls carry
+    the device tape's epilogues (TAPE_EPI)."""
+
+    def __init__(self, dev, seed=1, epilogues=False):
         import torch
         import oracle
         self.calls = []
         rng = oracle.Rng(seed)
         T = T_TOKENS
         self.bufs = []
+        self.epilogues = epilogues
+        extra = 0
         for name, K, N in LAYERS:
             X = torch.from_numpy(rng.gaussian(T * K)).to(dev)
-            W = torch.from_numpy(rng.gaussian(K * N, 0.02)).to(dev)
+            P = torch.from_numpy(rng.gaussian(K * N + (N if epilogues else 0), 0.02)).to(dev)
             dY = torch.from_numpy(rng.gaussian(T * N)).to(dev)
-            Y, dX, dW = (torch.zeros(n, device=dev) for n in (T * N, T * K, K * N))
-            self.bufs.append((X, W, dY, Y, dX, dW))
-            # (label, a, b, out, m, k, n)
-            self.calls.append((f"{name} fwd", dict(h=X), dict(h=W), dict(h=Y), T, K, N))
-            self.calls.append((f"{name} dX", dict(h=dY), dict(h=W, trans=True), dict(h=dX), T, N, K))
-            self.calls.append((f"{name} dW", dict(h=X, trans=True), dict(h=dY), dict(h=dW), K, T, N))
-        self.flops = sum(2 * m * k * n for _, _, _, _, m, k, n in self.calls)
+            Y, dX = (torch.zeros(n, device=dev) for n in (T * N, T * K))
+            G = torch.zeros(K * N + (N if epilogues else 0), device=dev)
+            R = None
+            fwd_epi, dw_epi = None, None
+            if epilogues:
+                relu, res = TAPE_EPI[name]
+                if res:
+                    R = torch.from_numpy(rng.gaussian(T * N)).to(dev)
+                fwd_epi = dict(bias=(P, K * N), relu=relu, residual=(R, 0) if res else None)
+                dw_epi = dict(accumulate=True, col_sum=(K * N, 0))
+                # bias read, residual read, dW read for +=, db read and written
+                extra += 4 * (N + (T * N if res else 0) + K * N + 2 * N)
+            self.bufs.append((X, P, dY, Y, dX, G, R))
+            # (label, a, b, out, m, k, n, epilogue)
+            self.calls.append((f"{name} fwd", dict(h=X), dict(h=P), dict(h=Y), T, K, N, fwd_epi))
+            self.calls.append((f"{name} dX", dict(h=dY), dict(h=P, trans=True), dict(h=dX), T, N, K, None))
+            self.calls.append((f"{name} dW", dict(h=X, trans=True), dict(h=dY), dict(h=G), K, T, N, dw_epi))
+        self.flops = sum(2 * m * k * n for _, _, _, _, m, k, n, _ in self.calls)
         # Algorithmic bytes: every distinct tensor of the set once (X, W, dY read; Y, dX, dW written).  X, W and dY
         # are each read by two GEMMs; counting them per GEMM (`per_gemm_bytes`) would double them.
-        self.bytes = sum(4 * 2 * (T * K + K * N + T * N) for _, K, N in LAYERS)
-        self.per_gemm_bytes = sum(4 * (m * k + k * n + m * n) for _, _, _, _, m, k, n in self.calls)
+        self.bytes = sum(4 * 2 * (T * K + K * N + T * N) for _, K, N in LAYERS) + extra
+        self.per_gemm_bytes = sum(4 * (m * k + k * n + m * n) for _, _, _, _, m, k, n, _ in self.calls)
 
     def call_fn(self, i, use_f16):
         import scratchtape_amd as st
-        _, a, b, o, m, k, n = self.calls[i]
+        _, a, b, o, m, k, n, epi = self.calls[i]
         A, B, O = st.MatRef(**a), st.MatRef(**b), st.MatRef(**o)
-        return lambda: st.matmul_with(A, B, O, 1, m, k, n, None, use_f16)
+        E = st.Epilogue(**epi) if epi else None
+        return lambda: st.matmul_with(A, B, O, 1, m, k, n, E, use_f16)
 
     def step_fn(self, use_f16):
         """The 15 GEMMs one call each (the reference's dispatch pattern), in set order."""
@@ -217,8 +240,9 @@ class StepSet:
 
     def args(self, i, use_f16):
         import scratchtape_amd as st
-        _, a, b, o, m, k, n = self.calls[i]
-        return (st.MatRef(**a), st.MatRef(**b), st.MatRef(**o), 1, m, k, n, None, use_f16)
+        _, a, b, o, m, k, n, epi = self.calls[i]
+        return (st.MatRef(**a), st.MatRef(**b), st.MatRef(**o), 1, m, k, n, st.Epilogue(**epi) if epi else None,
+                use_f16)
 
     def grouped_fn(self, use_f16):
         """The 15 GEMMs as one st_matmul_grouped call (they are independent here)."""
@@ -265,7 +289,7 @@ def bench_gemm_set(dev, stream, steps, warmup, use_f16):
         modes["grouped"]()  # the outputs the parity check reads come from the grouped launch
         torch.cuda.synchronize()
         per_call = []
-        for i, (label, _, _, _, m, k, n) in enumerate(ss.calls):
+        for i, (label, _, _, _, m, k, n, _) in enumerate(ss.calls):
             f = ss.call_fn(i, use_f16)
             f()
             ms = time_events(f, 50, stream)
@@ -305,7 +329,7 @@ def check_gemm_set(ss, use_f16):
     import oracle
     errs, errs32 = [], []
     with oracle.threads(host_threads()):
-        for label, a, b, o, m, k, n in ss.calls:
+        for label, a, b, o, m, k, n, _ in ss.calls:
             A = a["h"].cpu().numpy()
             B = b["h"].cpu().numpy()
             A = oracle.transpose(A.reshape(k, m)) if a.get("trans") else A.reshape(m, k)
@@ -321,12 +345,76 @@ def check_gemm_set(ss, use_f16):
     return max(errs), max(errs32)
 
 
+def check_epilogue_set(ss, use_f16=True):
+    """Parity of the step set with the tape's epilogues: every output buffer after ONE grouped call from known
+    contents (Y, dX zero; the gradient buffers [dW, db] filled with 0.5, so the accumulate and the column sums add to
+    them) against oracle.gemm with the same epilogue on the same host buffers.  Returns the largest scale-relative
+    errors over the 15 products and over the 5 bias gradients (column sums, in another summation order than the
+    oracle's)."""
+    import torch
+    import oracle
+    import scratchtape_amd as st
+    for X, P, dY, Y, dX, G, R in ss.bufs:
+        Y.zero_()
+        dX.zero_()
+        G.fill_(0.5)
+    st.matmul_grouped([ss.args(i, use_f16) for i in range(len(ss.calls))])
+    torch.cuda.synchronize()
+    errs, cs_errs = [], []
+    with oracle.threads(host_threads()):
+        for label, a, b, o, m, k, n, epi in ss.calls:
+            ref = lambda d: dict(off=0, stride=0, trans=int(bool(d.get("trans", False))), ld=0, group=1, inner=0)
+            out_h = np.zeros(o["h"].numel(), np.float32)
+            kw = {}
+            if epi:
+                if epi.get("bias"):
+                    kw["bias"] = (epi["bias"][0].cpu().numpy(), epi["bias"][1])
+                if epi.get("residual"):
+                    kw["residual"] = (epi["residual"][0].cpu().numpy(), 0)
+                kw["relu"] = bool(epi.get("relu", False))
+                if epi.get("accumulate"):
+                    out_h[:] = 0.5
+                    kw["accumulate"] = True
+                if epi.get("col_sum"):
+                    kw["col_sum"] = epi["col_sum"]
+            oracle.gemm(a["h"].cpu().numpy(), ref(a), b["h"].cpu().numpy(), ref(b), out_h, ref(o), 1, m, k, n,
+                        f16=use_f16, **kw)
+            got = o["h"].cpu().numpy()
+            rel = lambda g, w: float(np.max(np.abs(g - w)) / max(float(np.max(np.abs(w))), 1e-30))
+            errs.append(rel(got[:m * n], out_h[:m * n]))
+            if epi and epi.get("col_sum"):
+                cs_errs.append(rel(got[m * n:m * n + n], out_h[m * n:m * n + n]))
+    return max(errs), max(cs_errs)
+
+
+def bench_gemm_tape_epilogues(dev, stream, steps):
+    """The C3 f16 set as one grouped call with the device tape's epilogues (TAPE_EPI), graph-timed as the headline,
+    and its parity against the oracle."""
+    import torch
+    ss = StepSet(dev, epilogues=True)
+    err, cs_err = check_epilogue_set(ss)
+    fn = ss.grouped_fn(True)
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        spread = {}
+        ms = time_graph_steps(fn, steps, stream, spread=spread)
+    out = dict(graph_ms=round(ms, 5), graph_spread=spread, tflops=round(ss.flops / ms / 1e9, 2),
+               algorithmic_bytes=ss.bytes, hbm_gbs=round(ss.bytes / ms / 1e6, 1), parity_max_rel_err=err,
+               parity_col_sum_max_rel_err=cs_err,
+               epilogues={k: dict(relu=v[0], residual=v[1], bias=True) for k, v in TAPE_EPI.items()},
+               dw_epilogue="accumulate + bias gradient as column sums")
+    del ss
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_gemm_baseline(ss, budget_s=10.0):
     """The reference CPU path (NdArray::matmul, with the explicit transposes the tape makes) on full step sets:
     repeated for about `budget_s` seconds (at least 5 sets), one pinned core, median set time reported."""
     import oracle
     host = [(a["h"].cpu().numpy(), b["h"].cpu().numpy(), a.get("trans", False), b.get("trans", False), m, k, n)
-            for _, a, b, _, m, k, n in ss.calls]
+            for _, a, b, _, m, k, n, _ in ss.calls]
 
     def one_set():
         t0 = time.perf_counter()
@@ -816,6 +904,13 @@ def main():
                                    roofline=roofline("k_gemm_group f32 (+ k_sum_group)", ss32.flops, ss32.bytes, g32,
                                                      route="f32"),
                                    modes=t32, per_gemm=calls32, parity_max_rel_err=err32)
+        log("[bench] C3 f16 set with the device tape's epilogues")
+        extra["c3_f16_set_tape_epilogues"] = bench_gemm_tape_epilogues(dev, stream, args.steps)
+        log(f"[bench] tape-epilogue set: {extra['c3_f16_set_tape_epilogues']}")
+        te = extra["c3_f16_set_tape_epilogues"]
+        if te["parity_max_rel_err"] > 1e-5 or te["parity_col_sum_max_rel_err"] > 1e-4:
+            log("[bench] PARITY FAILURE: refusing to report")
+            sys.exit(3)
         log("[bench] C1 / C2 tape forms")
         extra["c1_256cube_f32"] = bench_tape_forms(dev, stream, 256, 256, 256, False)
         extra["c2_backward_f32"] = bench_tape_forms(dev, stream, 4096, 256, 1024, False)

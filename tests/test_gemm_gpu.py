@@ -391,3 +391,14 @@ def test_grouped_step_set_matches_the_oracle(dev, use_f16):
                 want16 = oracle.matmul(oracle.round_f16(a), oracle.round_f16(b))
                 err16 = float(np.max(np.abs(got - want16)) / np.max(np.abs(want16)))
                 assert err16 <= 1e-5, (i, err16)
+
+
+def test_grouped_step_set_with_tape_epilogues(dev):
+    """The C3 set at T = 4096 as one grouped call with the device tape's epilogues (gpu_step/tape.rs:180-189,
+    324-347): forward + bias (+ ReLU on FFN1, + residual after attention and FFN), dW += with the bias gradient as
+    column sums; every product within 1e-5 of the oracle on f16-rounded operands, the column sums within 1e-4."""
+    import bench
+    ss = bench.StepSet(dev, epilogues=True)
+    err, cs_err = bench.check_epilogue_set(ss)
+    assert err <= 1e-5, err
+    assert cs_err <= 1e-4, cs_err
