@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "dma_tile.h"
+#include "lanes.h"
 #include "gemm_dma.h"
 
 namespace {
@@ -535,6 +536,7 @@ using Tall16 = Cfg<256>;
 using Square16 = Cfg<128>;
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t lds_off(int r, int g) {
@@ -665,6 +667,61 @@ __device__ __forceinline__ void store_op(const OpRegs<R> (&v)[8], bool kc, char 
     }
 }
 
+// The B operand (TN = 128 rows: columns of B) moves in 16-byte loads, four
+// per lane and stage, so that a stage of both operands is 12 load
+// instructions per producer lane instead of 16 (every load instruction costs
+// the texture addresser about the same whatever its width).  RC (rows of B
+// contiguous, i.e. B not transposed): lane id holds columns 4 (id % 32) .. + 3
+// on k-lines 4 (id / 32) + n, n < 4; KC: row id / 8 + 32 n, k 4 (id % 8) .. + 3.
+template <int R>
+__device__ __forceinline__ void op_ref_b(OpRef &o, bool kc, const float *base, int64_t ld, int id) {
+    static_assert(R == TN, "the B panel");
+    o.kc = kc;
+    o.base = reinterpret_cast<const char *>(base);
+    o.sh = 0;
+    o.msk = 0;
+    if (kc) {
+        o.step = 4 * BK;
+        o.pair = (int32_t)(32 * ld * 4);
+        o.off = (uint32_t)((id >> 3) * ld * 4 + 16 * (id & 7));
+    } else {
+        o.step = (int32_t)(BK * ld * 4);
+        o.pair = (int32_t)(ld * 4);
+        o.off = (uint32_t)(4 * (id >> 5) * ld * 4 + 16 * (id & 31));
+    }
+}
+
+__device__ __forceinline__ void load_b(u32x4 (&v)[4], const OpRef &o, int st) {
+    const int32_t s0 = st * o.step;
+    const __amdgpu_buffer_rsrc_t r = rsrc(o.base);
+#pragma unroll
+    for (int n = 0; n < 4; n++) v[n] = __builtin_amdgcn_raw_buffer_load_b128(r, o.off, s0 + n * o.pair, 0);
+}
+
+// Rounds a loaded stage of B to f16 and writes it to its LDS region: half of
+// a k-group (4 k, 8 bytes) per column (RC) or row (KC) and load.
+__device__ __forceinline__ void store_b(const u32x4 (&v)[4], bool kc, char *region, int id) {
+    if (kc) {
+        const int c8 = id & 7;
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (_Float16)f_(v[n][e]);
+            *reinterpret_cast<half4 *>(region + lds_off((id >> 3) + 32 * n, c8 >> 1) + 8 * (c8 & 1)) = h;
+        }
+    } else {
+        const int kq = id >> 5, cg = id & 31;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            half4 h;
+#pragma unroll
+            for (int n = 0; n < 4; n++) h[n] = (_Float16)f_(v[n][e]);
+            *reinterpret_cast<half4 *>(region + lds_off(4 * cg + e, kq >> 1) + 8 * (kq & 1)) = h;
+        }
+    }
+}
+
 template <class C>
 __device__ __forceinline__ void locate16(const GroupArgs &ga, const int32_t *cum, int x, int j, int lane, int id, Unit16 &u) {
     const int count = ga.count;
@@ -693,7 +750,7 @@ __device__ __forceinline__ void locate16(const GroupArgs &ga, const int32_t *cum
     const float *b = uni(g.b + zoff(u.zb, g.b_group, g.b_stride, g.b_inner) +
                          (bkc ? (int64_t)u.col0 * ldb + kbeg : (int64_t)kbeg * ldb + u.col0));
     op_ref<C::TM>(u.a, akc, a, lda, id);
-    op_ref<TN>(u.b, bkc, b, ldb, id);
+    op_ref_b<TN>(u.b, bkc, b, ldb, id);
 }
 
 // grid: a multiple of 8 workgroups, at most one per CU.  Every unit has at
@@ -742,7 +799,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
 
     // ---- producer state: NSL register sets --------------------------------
     OpRegs<TM> va[NSL][8];
-    OpRegs<TN> vb[NSL][8];
+    u32x4 vb[NSL][4];
     // The load cursor: the unit the next loads come from (its operand
     // references by value, lu = 0 cur, 1 nxt) and its stage.  Kept apart from
     // cur / nxt so that the lane offsets the loads use change only when the
@@ -752,13 +809,13 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
     bool lvalid = true;
     // Loads the cursor's stage into register set S.  Past the workgroup's
     // last stage the loads still go out (re-reading the last unit's first
-    // stage, never multiplied), so that every step has the same 16 loads in
+    // stage, never multiplied), so that every step has the same 12 loads in
     // flight and the compiler's waits before each conversion count the two
     // younger stages' loads exactly.
     auto issue = [&](auto set_c) __attribute__((always_inline)) {
         constexpr int S = decltype(set_c)::value;
         load_op<TM>(va[S], la, lvalid ? lst : 0);
-        load_op<TN>(vb[S], lb, lvalid ? lst : 0);
+        load_b(vb[S], lb, lvalid ? lst : 0);
         if (lvalid && ++lst == lnst) {
             // The loads run at most 3 stages ahead of the multiplication and
             // every unit has 4 or more: only cur's loads can run out here.
@@ -784,16 +841,23 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         const bool cs = !none && (in_cur ? cur.cs : nxt.cs);
         const int P = none ? NSL : S;
         store_op<TM>(va[S], akc, lds + P * SLOT, id);
-        store_op<TN>(vb[S], bkc, lds + P * SLOT + SA, id);
+        store_b(vb[S], bkc, lds + P * SLOT + SA, id);
         if (cs) {
             // B is row-contiguous here (the f16 route sums columns only then):
-            // this lane holds columns 2 (id % 64) + w2 on k 8 (id / 64) .. + 7.
+            // this lane holds columns 4 (id % 32) + e on k 4 (id / 32) .. + 3,
+            // and lane id ^ 32 the other half of the k-group id / 64.  The
+            // group's 8 values of a column are added in k order (the lower
+            // half's sum handed up), as the single-GEMM kernel adds them.
 #pragma unroll
-            for (int w2 = 0; w2 < 2; w2++) {
+            for (int e = 0; e < 4; e++) {
                 float p = 0.f;
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) p += f_(vb[S][jj][w2]);
-                csp[P][id >> 6][2 * (id & 63) + w2] = p;
+                for (int n = 0; n < 4; n++) p += f_(vb[S][n][e]);
+                const float lo = st::xor_lane(p, 32, lane);
+                float q = lo;
+#pragma unroll
+                for (int n = 0; n < 4; n++) q += f_(vb[S][n][e]);
+                if (lane >= 32) csp[P][id >> 6][4 * (id & 31) + e] = q;
             }
         }
     };
@@ -917,10 +981,10 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group16(GroupArgs ga) {
         // stage q + 1 into slot S + 1.
         auto step = [&](auto set_c) __attribute__((always_inline)) -> bool {
             constexpr int S = decltype(set_c)::value;
-            // Stages q + 1 and q + 2 (16 loads each) are in flight, stage q's
+            // Stages q + 1 and q + 2 (12 loads each) are in flight, stage q's
             // loads are done: a no-op wait that tells the compiler so, which it
             // cannot work out through the loop's back edge by itself.
-            wait_vm<32>();
+            wait_vm<24>();
             issue(set_c);
             constexpr int S1 = (S + 1) % NSL;
             const bool none = !(st + 1 < cur.nst) && nxt.p < 0;
