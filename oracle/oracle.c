@@ -211,6 +211,8 @@ void orc_gemm(const float *a_buf, const orc_matref *ar, const float *b_buf, cons
         int64_t a0 = mat_base(ar, z), b0 = mat_base(br, z);
         int64_t o0 = (z / (orf->group > 0 ? orf->group : 1)) * orf->stride +
                      (z % (orf->group > 0 ? orf->group : 1)) * orf->inner;
+        /* Rows split over threads: each element's arithmetic is unchanged. */
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
         for (int64_t i = 0; i < m; i++) {
             for (int64_t j = 0; j < n; j++) {
                 float s = 0.0f;

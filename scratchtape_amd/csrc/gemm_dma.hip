@@ -95,8 +95,9 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
         for (int j = 0; j < LB; j++) dma16(bbase + boff[j] + st * bstep, base + SA * 4 + (wave_u * LB + j) * 1024);
     };
 
-    f32x4 acc[FM][FN];      // f32 route: 16 x 16 blocks
-    f32x16 acc2[M32][N32];  // f16 route: 32 x 32 blocks
+    constexpr int AM = M32 > 0 ? M32 : 1, AN = N32 > 0 ? N32 : 1;  // (32 x 32 f32 tiles have no 32 x 32 blocks)
+    f32x4 acc[FM][FN];    // f32 route: 16 x 16 blocks
+    f32x16 acc2[AM][AN];  // f16 route: 32 x 32 blocks
     if constexpr (F16) {
 #pragma unroll
         for (int i = 0; i < M32; i++)
@@ -337,13 +338,15 @@ bool dma_plan(const st::DmaGemm &d, DmaPlan &p) {
     struct Cfg {
         int bm, bn;
     };
-    const Cfg cands[] = {{128, 128}, {128, 64}, {64, 64}};
+    // 32 x 32 (f32 route only: the f16 route's MFMA blocks are 32 x 32 per
+    // wave) spreads a small product over 4x the workgroups of 64 x 64.
+    const Cfg cands[] = {{128, 128}, {128, 64}, {64, 64}, {32, 32}};
     int best = -1;
     int64_t best_splits = 1;
     double best_t = 0;
-    for (int c = 0; c < 3; c++) {
+    for (int c = 0; c < 4; c++) {
         const int bm = cands[c].bm, bn = cands[c].bn;
-        if (m % bm || n % bn) continue;
+        if (m % bm || n % bn || (bm == 32 && d.f16)) continue;
         const int64_t tiles = batch * (m / bm) * (n / bn);
         for (int64_t sp = 1; sp <= 32; sp *= 2) {
             if (sp > 1 && (!can_split || k / sp < 4 * BK)) break;
@@ -433,14 +436,16 @@ bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
         g.out = part;
         g.cs = cs_part;
     }
-    // Ring depths: 128 KB, 96 KB and 64 KB of LDS per workgroup.
+    // Ring depths: 128 KB, 96 KB, 64 KB and 8 KB per stage of 32 x 32.
     KernelFn fn;
     if (bm == 128 && bn == 128)
         fn = pick2<128, 128, 4>(d.f16, d.ta, d.tb);
     else if (bm == 128)
         fn = pick2<128, 64, 4>(d.f16, d.ta, d.tb);
-    else
+    else if (bm == 64)
         fn = pick2<64, 64, 4>(d.f16, d.ta, d.tb);
+    else
+        fn = pick<32, 32, 4, false>(d.ta, d.tb);
     hipLaunchKernelGGL(fn, dim3((unsigned)(n / bn), (unsigned)(m / bm), (unsigned)(batch * splits)), dim3(THREADS), 0,
                        stream, g);
     hipError_t e = hipGetLastError();

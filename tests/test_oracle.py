@@ -506,12 +506,20 @@ def test_knn_search_equals_brute_force_and_handles_edges():
 
 
 def test_thread_count_does_not_change_results():
-    """The all-cores CPU baseline runs the same oracle over several threads: matmul, transpose and knn_search
-    split rows (queries) only, so their outputs are bit-identical to the single-threaded ones."""
+    """The all-cores CPU baseline runs the same oracle over several threads: matmul, transpose, gemm and
+    knn_search split rows (queries) only, so their outputs are bit-identical to the single-threaded ones."""
     rng = np.random.default_rng(77)
     a = rng.standard_normal((300, 130)).astype(np.float32)
     b = rng.standard_normal((130, 70)).astype(np.float32)
-    one = oracle.matmul(a, b), oracle.transpose(a)
+    bias = rng.standard_normal(70).astype(np.float32)
+    ref = lambda trans: dict(off=0, stride=0, trans=trans, ld=0, group=1, inner=0)
+
+    def gemm():
+        out = np.full(300 * 70 + 70, 0.5, np.float32)
+        # Aᵀ read in place from a transposed copy, f16 operands, bias + ReLU, +=, column sums.
+        return oracle.gemm(np.ascontiguousarray(a.T), ref(1), b, ref(0), out, ref(0), 1, 300, 130, 70,
+                           bias=(bias, 0), relu=True, accumulate=True, col_sum=(300 * 70, 0), f16=True)
+    one = oracle.matmul(a, b), oracle.transpose(a), gemm()
     d, ncells, nq = 256, 10, 13
     sizes = rng.integers(50, 300, ncells)
     cell_start = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
@@ -520,7 +528,7 @@ def test_thread_count_does_not_change_results():
     probes = np.stack([rng.choice(ncells, 3, replace=False) for _ in range(nq)]).astype(np.int32)
     one_knn = oracle.knn_search(codes, scales, cell_start, queries, probes, 128)
     with oracle.threads(4):
-        many = oracle.matmul(a, b), oracle.transpose(a)
+        many = oracle.matmul(a, b), oracle.transpose(a), gemm()
         many_knn = oracle.knn_search(codes, scales, cell_start, queries, probes, 128)
     assert oracle.lib().orc_get_threads() == 1
     for x, y in zip(one + one_knn, many + many_knn):
