@@ -842,7 +842,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "gemm", "knn"], default="all")
+    ap.add_argument("--only", choices=["all", "gemm", "knn", "gemm_set"], default="all",
+                    help="gemm_set: only the headline f16 step set as one grouped call (warm-up, the graph-timed "
+                         "steps, parity), one JSON line: the workload its rocprofv3 counter summary is taken on")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -870,6 +872,20 @@ def main():
     prop = torch.cuda.get_device_properties(dev)
     extra = {"device": {"name": prop.name}, "host_cpu": cpu_model(), "nproc": os.cpu_count()}
     result = None
+
+    if args.only == "gemm_set":
+        ss = StepSet(dev)
+        fn = ss.grouped_fn(True)
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            ms = time_graph_steps(fn, args.steps, stream)
+        err, _ = check_gemm_set(ss, True)
+        print(json.dumps(dict(workload="d_model-256 step GEMM set, f16 route, one grouped call", steps=args.steps,
+                              ms_per_step=round(ms, 5), tflops=round(ss.flops / ms / 1e9, 2),
+                              parity_max_rel_err=err)))
+        sys.exit(0 if err <= 1e-5 else 3)
 
     if args.only in ("all", "gemm"):
         log("[bench] C3 step GEMM set, f16-in/f32-acc")

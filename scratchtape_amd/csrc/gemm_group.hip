@@ -711,13 +711,34 @@ __device__ __forceinline__ void store_b(const u32x4 (&v)[4], bool kc, char *regi
             *reinterpret_cast<half4 *>(region + lds_off((id >> 3) + 32 * n, c8 >> 1) + 8 * (c8 & 1)) = h;
         }
     } else {
-        const int kq = id >> 5, cg = id & 31;
+        // Lanes l and l + 32 of a wave hold k 0-3 and k 4-7 of one k-group
+        // (kq even / odd) for the same four columns.  One v_permlane32_swap
+        // per dword trades column e of the upper lane for column e + 2 of the
+        // lower one, so the lower lane writes whole 8-k groups of columns 0, 1
+        // and the upper lane of columns 2, 3: 16-byte writes that each touch
+        // every bank once per 16 lanes (8-byte halves of a group left every
+        // half-wave on half of the banks).
+        const int kq = id >> 5, cg = id & 31, up = kq & 1;
+        uint32_t h[4][2];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            half4 h;
+            half4 t;
 #pragma unroll
-            for (int n = 0; n < 4; n++) h[n] = (_Float16)f_(v[n][e]);
-            *reinterpret_cast<half4 *>(region + lds_off(4 * cg + e, kq >> 1) + 8 * (kq & 1)) = h;
+            for (int n = 0; n < 4; n++) t[n] = (_Float16)f_(v[n][e]);
+            const u32x2 w = __builtin_bit_cast(u32x2, t);
+            h[e][0] = w[0];
+            h[e][1] = w[1];
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            u32x4 g;
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                const auto r = __builtin_amdgcn_permlane32_swap(h[e][d], h[e + 2][d], false, false);
+                g[d] = r[0];
+                g[2 + d] = r[1];
+            }
+            *reinterpret_cast<u32x4 *>(region + lds_off(4 * cg + e + 2 * up, kq >> 1)) = g;
         }
     }
 }
