@@ -841,12 +841,14 @@ __device__ __forceinline__ void merge_lists(lds_u64 *A, const lds_u64 *B, int la
 // the k-th smallest key of any one of its cells bounds it); every finished
 // (query, cell) list lowers it, and every later unit of the query drops keys
 // at or above it from the start.  A bound read stale is larger, never wrong.
-// Four waves per workgroup, three workgroups per CU (the register budget is
-// capped at 168 VGPRs for that; 33 spill, yet 4,096 queries x 8 probes ran
-// 1.75 ms against 1.88 ms with two per CU at 207 VGPRs, and four per CU, 72
-// spilled, 1.98 ms), so that one workgroup's set-up and final merges run
-// while the others stream.
-constexpr int CW = 4;                       // waves per cell-major workgroup
+// Two waves per workgroup, six workgroups per CU (12 waves; the register
+// budget is capped at 168 VGPRs for that and 32 spill): one workgroup's unit
+// set-up and final merges then idle a sixth of the CU's loads in flight, and
+// each unit streams twice as long as with four waves.  4,096 queries x 8
+// probes: 1.62 ms, against 1.74 ms with four-wave workgroups three per CU,
+// 1.88 ms two per CU at 207 VGPRs, 1.98 ms four per CU (72 spilled) and
+// 1.67 ms with one-wave workgroups twelve per CU.
+constexpr int CW = 2;                       // waves per cell-major workgroup
 constexpr int CTH = CW * 64;
 constexpr int E8C = (KMAX + CW - 1) / CW;   // each wave's published rank
 __global__ __launch_bounds__(CTH) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_search_cells(const uint8_t *codes, const float *scales,
@@ -891,11 +893,11 @@ __global__ __launch_bounds__(CTH) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                                                      __HIP_MEMORY_SCOPE_AGENT)
                                  : 0ull;
         if (tid < QG * CW) s_e8[tid / CW][tid % CW] = NONE;
-        if (wave < n) {
-            const QInfo qi = quantize_query(queries + (int64_t)(s_u.qp[wave] / nprobe) * D, lane, s_Q + wave * D);
+        for (int s = wave; s < n; s += CW) {
+            const QInfo qi = quantize_query(queries + (int64_t)(s_u.qp[s] / nprobe) * D, lane, s_Q + s * D);
             if (lane == 0) {
-                s_qs[wave] = qi.qs;
-                s_sq[wave] = qi.sq;
+                s_qs[s] = qi.qs;
+                s_sq[s] = qi.sq;
             }
         }
         __syncthreads();
@@ -1234,8 +1236,8 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
     }
-    // Persistent workgroups, three per CU (those that find no unit left exit).
-    const unsigned wgs = (unsigned)std::min<int64_t>(npairs, 3 * (int64_t)cus);
+    // Persistent workgroups, six per CU (those that find no unit left exit).
+    const unsigned wgs = (unsigned)std::min<int64_t>(npairs, 6 * (int64_t)cus);
     hipLaunchKernelGGL(k_search_cells, dim3(wgs), dim3(CTH), 0, s, codes, scales, cell_start, ncells, queries,
                        (int32_t)nprobe, (int32_t)k, units, hdr, qtau, parts);
     ST_LAUNCH_CHECK();
