@@ -989,7 +989,14 @@ def main():
         extra["c5_knn_4096q"] = dict(ms_per_batch=round(wms, 5), queries=4096, pairs_per_batch=wb["pairs"],
                                      g_keys_per_s=round(wb["pairs"] / wms / 1e6, 3),
                                      distinct_cell_bytes=wb["bytes"], hbm_gbs=round(wgbs, 1),
-                                     hbm_frac=round(wgbs / PEAK["hbm_gbs"], 4), steps_per_graph=wsteps)
+                                     hbm_frac=round(wgbs / PEAK["hbm_gbs"], 4), steps_per_graph=wsteps,
+                                     roofline=dict(kernel="cell-major scan (k_group_* + k_search_cells + "
+                                                          "k_merge_parts)", bound="hbm", achieved=round(wgbs, 1),
+                                                   peak=PEAK["hbm_gbs"], unit="GB/s",
+                                                   frac=round(wgbs / PEAK["hbm_gbs"], 4),
+                                                   traffic=traffic_for("k_search cell-major 4096q",
+                                                                       "scratchtape_amd/csrc/knn.hip"),
+                                                   algorithmic_bytes=int(wb["bytes"])))
         del wb
         log("[bench] C5 probe selection (12288 centroids, 256 queries x 8)")
         pb = ProbeBench(dev, [b["q"] for b in kb.batches])
