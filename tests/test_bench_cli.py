@@ -26,6 +26,7 @@ def test_traffic_is_quoted_only_for_the_profiled_source():
     for key, e in table.items():
         src = {"k_gemm_group16 f16 step set": "scratchtape_amd/csrc/gemm_group.hip",
                "k_search": "scratchtape_amd/csrc/knn.hip", "k_search masked": "scratchtape_amd/csrc/knn.hip",
+               "k_search cell-major 4096q": "scratchtape_amd/csrc/knn.hip",
                "st_knn_probe": "scratchtape_amd/csrc/knn_probe.hip", "k_attn fused step": "scratchtape_amd/csrc/attn.hip",
                "k_ln step": "scratchtape_amd/csrc/rows.hip"}[key]
         want = int(e["fetch_bytes"] + e["write_bytes"]) if e["source_sha256_16"] == bench.source_hash(src) else None
