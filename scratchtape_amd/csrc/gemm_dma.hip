@@ -292,6 +292,93 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ pa
     }
 }
 
+// Small products (no column sums, m % 16 = n % 16 = 0, k % 256 = 0, so each
+// wave's quarter of k is whole passes of 64): one 16 x 16 output tile per
+// workgroup, so that a 256 x 256
+// product spreads over 256 CUs (32 x 32 tiles leave 64 of them 0.85 us of
+// matrix-core work each).  The four waves split k into quarters, taken in
+// passes of 64; in a pass lane group q (lanes 16 q .. 16 q + 15) holds k
+// p0 + 16 q .. + 15 of its A row and B column, so MFMA step j sums k
+// {p0 + j, p0 + 16 + j, p0 + 32 + j, p0 + 48 + j}.  Every load of a pass is
+// issued before the first MFMA.  The waves' partial tiles are added in wave
+// order through LDS (deterministic), then the epilogue in the reference's
+// order.  f32 route: v_mfma_f32_16x16x4_f32, one k per lane group and step;
+// f16 route: the operands rounded to f16 (nearest even) and two
+// v_mfma_f32_16x16x32_f16 per pass, element e of the lane's 16 k in the
+// first (e < 8) or second instruction (A and B agree on the order).  Lane l
+// ends with rows 4 (l / 16) + e, column l % 16 of the tile.
+template <bool TA, bool TB, bool F16>
+__global__ __launch_bounds__(256) void k_gemm_tiny(KArgs g) {
+    __shared__ f32x4 part[3][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, q = lane >> 4;
+    const int64_t zb = blockIdx.z;
+    const int row0 = blockIdx.y * 16, col0 = blockIdx.x * 16;
+    const float *A = g.a + zoff(zb, g.a_group, g.a_stride, g.a_inner);
+    const float *B = g.b + zoff(zb, g.b_group, g.b_stride, g.b_inner);
+    const int kq = g.k / 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int p0 = wave * kq; p0 < (wave + 1) * kq; p0 += 64) {
+        const int kb = p0 + 16 * q;
+        float a[16], b[16];
+        if constexpr (!TA) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(A + (int64_t)(row0 + r) * g.lda + kb + 4 * i);
+#pragma unroll
+                for (int e = 0; e < 4; e++) a[4 * i + e] = v[e];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) a[j] = A[(int64_t)(kb + j) * g.lda + row0 + r];
+        }
+        if constexpr (TB) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(B + (int64_t)(col0 + r) * g.ldb + kb + 4 * i);
+#pragma unroll
+                for (int e = 0; e < 4; e++) b[4 * i + e] = v[e];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) b[j] = B[(int64_t)(kb + j) * g.ldb + col0 + r];
+        }
+        if constexpr (F16) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                half8 ah, bh;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    ah[e] = (_Float16)a[8 * h + e];
+                    bh[e] = (_Float16)b[8 * h + e];
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], acc, 0, 0, 0);
+        }
+    }
+    if (wave > 0) part[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave > 0) return;
+    acc = ((acc + part[0][lane]) + part[1][lane]) + part[2][lane];
+    const int64_t o0 = zoff(zb, g.o_group, g.o_stride, g.o_inner);
+    const int col = col0 + r;
+    const float bv = g.bias ? g.bias[zb * g.bias_stride + col] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int64_t idx = o0 + (int64_t)(row0 + 4 * q + e) * g.ldo + col;
+        float v = acc[e];
+        if (g.bias) v += bv;
+        if (g.relu && v < 0.f) v = 0.f;
+        if (g.mask && g.mask[idx] <= 0.f) v = 0.f;
+        if (g.res) v += g.res[idx];
+        if (g.accumulate) v += g.out[idx];
+        g.out[idx] = v;
+    }
+}
+
 using KernelFn = void (*)(KArgs);
 
 template <int BM, int BN, int NS, bool F16>
@@ -315,6 +402,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 struct DmaPlan {
     int bm, bn;
     int64_t splits, slice_k;
+    bool tiny;  // k_gemm_tiny instead of k_gemm_dma
 };
 
 bool dma_plan(const st::DmaGemm &d, DmaPlan &p) {
@@ -362,11 +450,29 @@ bool dma_plan(const st::DmaGemm &d, DmaPlan &p) {
             }
         }
     }
+    // A small product (at most 1,024 tiles of 16 x 16, k <= 1,024, no column
+    // sums) that no tile fits, or whose best tiling leaves most CUs idle,
+    // takes 16 x 16 tiles when that gives at least twice the workgroups.
+    // Larger outputs stay on the bigger tiles, which re-read the operands
+    // less.
+    const int64_t tiny_wgs = batch * (m / 16) * (n / 16);
+    const bool tiny_ok = !d.has_cs && m % 16 == 0 && n % 16 == 0 && k % 256 == 0 && k <= 1024 &&
+                         tiny_wgs <= 1024;
+    if (best >= 0) {
+        p.bm = cands[best].bm;
+        p.bn = cands[best].bn;
+        p.slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
+        p.splits = cdiv(k, p.slice_k);
+    }
+    const int64_t dma_wgs = best >= 0 ? batch * (m / p.bm) * (n / p.bn) * p.splits : 0;
+    p.tiny = tiny_ok && (best < 0 || (dma_wgs < 256 && tiny_wgs >= 2 * dma_wgs));
+    if (p.tiny) {
+        p.bm = p.bn = 16;
+        p.splits = 1;
+        p.slice_k = k;
+        return true;
+    }
     if (best < 0) return false;
-    p.bm = cands[best].bm;
-    p.bn = cands[best].bn;
-    p.slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
-    p.splits = cdiv(k, p.slice_k);
     return !(batch * p.splits > 65535 || m / p.bm > 65535 || n / p.bn > INT32_MAX);
 }
 
@@ -435,6 +541,20 @@ bool gemm_dma(const DmaGemm &d, hipStream_t stream, st_status *status) {
         cs_part = part + pfl;
         g.out = part;
         g.cs = cs_part;
+    }
+    if (plan.tiny) {
+        KernelFn tf;
+        if (d.f16)
+            tf = d.ta ? (d.tb ? &k_gemm_tiny<true, true, true> : &k_gemm_tiny<true, false, true>)
+                      : (d.tb ? &k_gemm_tiny<false, true, true> : &k_gemm_tiny<false, false, true>);
+        else
+            tf = d.ta ? (d.tb ? &k_gemm_tiny<true, true, false> : &k_gemm_tiny<true, false, false>)
+                      : (d.tb ? &k_gemm_tiny<false, true, false> : &k_gemm_tiny<false, false, false>);
+        hipLaunchKernelGGL(tf, dim3((unsigned)(n / 16), (unsigned)(m / 16), (unsigned)batch), dim3(THREADS), 0,
+                           stream, g);
+        const hipError_t e = hipGetLastError();
+        *status = e == hipSuccess ? ST_OK : fail(ST_ERR_HIP, "GEMM launch failed: %s", hipGetErrorString(e));
+        return true;
     }
     // Ring depths: 128 KB, 96 KB, 64 KB and 8 KB per stage of 32 x 32.
     KernelFn fn;
