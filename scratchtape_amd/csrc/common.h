@@ -57,6 +57,10 @@ class ScratchScope {
 // 1 when a gfx950 device is current; otherwise sets the error.
 bool device_ok();
 
+// The current device's compute-unit count (cached per device; 256 when the
+// query fails).
+int device_cus();
+
 inline hipStream_t stream_of(st_stream s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace st

@@ -1134,14 +1134,6 @@ bool can_split(const st::DmaGemm &d) {
 constexpr uint32_t DEFAULT_WAIT_POLLS = 1u << 20;
 std::atomic<uint32_t> g_wait_polls{DEFAULT_WAIT_POLLS};
 
-int cu_count() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 256;
-    return cus;
-}
-
 }  // namespace
 
 namespace st {
@@ -1272,11 +1264,7 @@ size_t group_part_floats(const st::DmaGemm *items, int count, const std::vector<
     return f;
 }
 
-int group_cus() {
-    static thread_local int cus_cached = 0;
-    if (!cus_cached) cus_cached = cu_count();
-    return cus_cached;
-}
+int group_cus() { return st::device_cus(); }
 
 template <class C>
 st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupArgs), hipStream_t stream) {

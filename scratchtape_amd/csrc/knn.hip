@@ -1229,13 +1229,7 @@ extern "C" st_status st_knn_search_ivf_2bit(const uint8_t *codes, const float *s
     hipLaunchKernelGGL(k_group_scatter, dim3(pb), dim3(256), 0, s, probes, (int32_t)nq, (int32_t)nprobe, ncells, cnt,
                        fill, ubase, units);
     ST_LAUNCH_CHECK();
-    static thread_local int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
+    const int cus = st::device_cus();
     // Persistent workgroups, six per CU (those that find no unit left exit).
     const unsigned wgs = (unsigned)std::min<int64_t>(npairs, 6 * (int64_t)cus);
     hipLaunchKernelGGL(k_search_cells, dim3(wgs), dim3(CTH), 0, s, codes, scales, cell_start, ncells, queries,

@@ -1,4 +1,5 @@
 // Library runtime: error reporting, device check, scratch arena, version.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -141,6 +142,27 @@ bool device_ok() {
     }
     checked_dev = dev;
     return true;
+}
+
+int device_cus() {
+    constexpr int MAX_DEVICES = 64;
+    static std::atomic<int> cached[MAX_DEVICES];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (dev >= 0 && dev < MAX_DEVICES) {
+        const int c = cached[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (dev >= 0 && dev < MAX_DEVICES) cached[dev].store(cus, std::memory_order_relaxed);
+    return cus;
 }
 
 }  // namespace st
