@@ -144,6 +144,8 @@ DMA_CASES = [
     # m, n multiples of 32 but not of 64: the f32 route's 32 x 32 tiles (the f16 route takes k_gemm)
     (1, 96, 256, 160, True, True, True, True, True, False),
     (2, 32, 1024, 96, False, False, False, False, True, True),
+    # n = 48: no DMA tile fits; batched 16 x 16 tiles (k_gemm_tiny), f32 and f16 routes
+    (2, 64, 256, 48, True, False, True, False, True, False),
 ]
 
 
