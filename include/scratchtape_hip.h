@@ -231,9 +231,9 @@ st_status st_knn_key_norms_2bit(const uint8_t *codes, const float *scales, int64
  * padding), out_dist [nq, k] = max(|q^|^2 + dist, 0) (+inf padding).
  * All pointers are device pointers; d == 256; the store holds fewer than
  * 2^32 keys (cell_start[ncells] < 2^32: key indices are 32-bit inside the
- * top-k keys).  A batch whose nq * nprobe probes reach ncells or more (each
- * cell probed once or more on average; the reference groups such batches by
- * cell, ivf.rs:491-499) is scanned cell-major: each probed cell is read once
+ * top-k keys).  A batch whose nq * nprobe probes reach 2/3 of ncells or
+ * more (each cell probed 2/3 of a time or more on average; the reference
+ * groups such batches by cell, ivf.rs:491-499) is scanned cell-major: each probed cell is read once
  * for up to four of its queries, with the per-pair lists in the library's
  * kNN scratch arena (nq * nprobe * 1 KiB; serialise such calls per device,
  * and run one before capturing a graph).  Smaller batches use no scratch. */
