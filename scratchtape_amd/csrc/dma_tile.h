@@ -187,6 +187,23 @@ __device__ __forceinline__ void frag(const float *t, int r, int g, float (&x)[8]
     }
 }
 
+// acc + src[0] + src[step] + .. + src[(splits - 1) step], added in that order
+// (the deterministic split-k sum), with the loads of up to 16 slices issued
+// before the first add: one memory round trip per 16 slices, not one per slice.
+template <class P, class T>
+__device__ __forceinline__ T sum_slices(P src, int64_t step, int splits, T acc) {
+    for (int s0 = 0; s0 < splits; s0 += 16) {
+        T v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (s0 + j < splits) v[j] = src[(s0 + j) * step];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (s0 + j < splits) acc += v[j];
+    }
+    return acc;
+}
+
 __device__ __forceinline__ int64_t zoff(int64_t z, int64_t group, int64_t stride, int64_t inner) {
     return (z / group) * stride + (z % group) * inner;
 }

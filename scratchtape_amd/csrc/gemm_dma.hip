@@ -266,7 +266,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm_dma(KArgs g) {
 }
 
 // out[b] (+)= sum over s (ascending) of partial[b][s], 4 elements per thread;
-// then the column-sum partials into their destination (always +=).
+// then the column-sum partials into their destination (always +=).  Each
+// thread's slice loads are in flight together (sum_slices).
 __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ part, float *out, int64_t mn,
                                                     int32_t splits, int64_t o_stride, int64_t batch,
                                                     int32_t accumulate, const float *cs_part, float *cs_dst,
@@ -274,10 +275,9 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ pa
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t q = mn / 4;
     if (e < batch * q) {
-        const int64_t b = e / q, i = e % q;
+        const int64_t b = batch == 1 ? 0 : e / q, i = batch == 1 ? e : e % q;
         const f32x4 *p = reinterpret_cast<const f32x4 *>(part) + b * splits * q + i;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < splits; s++) v += p[s * q];
+        f32x4 v = sum_slices(p, q, splits, f32x4{0.f, 0.f, 0.f, 0.f});
         f32x4 *o = reinterpret_cast<f32x4 *>(out + b * o_stride) + i;
         if (accumulate) v += *o;
         *o = v;
@@ -285,8 +285,7 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ pa
         const int64_t c = e - batch * q;
         if (c < batch * n) {
             const int64_t b = c / n, j = c % n;
-            float v = 0.f;
-            for (int s = 0; s < splits; s++) v += cs_part[(b * splits + s) * n + j];
+            const float v = sum_slices(cs_part + b * splits * n + j, n, splits, 0.f);
             cs_dst[b * cs_stride + j] += v;
         }
     }

@@ -1084,7 +1084,8 @@ struct SumArgs {
 static_assert(sizeof(SumArgs) % 4 == 0, "copied to LDS as 32-bit words");
 
 // The split GEMMs' partial sums, one thread per 4 outputs (then one per
-// column sum), as k_sum_slices; thread ranges per GEMM start at t0.  The
+// column sum), as k_sum_slices (each thread's slice loads in flight
+// together); thread ranges per GEMM start at t0.  The
 // arguments are copied to LDS first (as in k_gemm_group).
 __global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
     __shared__ SumArgs ssa;
@@ -1101,19 +1102,17 @@ __global__ __launch_bounds__(256) void k_sum_group(SumArgs sa) {
     const int64_t local = e - s.t0;
     if (local < 0) return;
     if (local < s.batch * s.mn4) {
-        const int64_t b = local / s.mn4, i = local % s.mn4;
+        const int64_t b = s.batch == 1 ? 0 : local / s.mn4, i = s.batch == 1 ? local : local % s.mn4;
         const gptr<const f32x4> src = (gptr<const f32x4>)s.part + b * s.splits * s.mn4 + i;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        for (int sl = 0; sl < s.splits; sl++) v += src[sl * s.mn4];
+        f32x4 v = sum_slices(src, s.mn4, s.splits, f32x4{0.f, 0.f, 0.f, 0.f});
         const gptr<f32x4> o = (gptr<f32x4>)(s.out + b * s.o_stride) + i;
         if (s.accumulate) v += *o;
         *o = v;
     } else if (s.cs_part) {
         const int64_t c = local - s.batch * s.mn4;
         if (c < s.batch * s.n) {
-            const int64_t b = c / s.n, jn = c % s.n;
-            float v = 0.f;
-            for (int sl = 0; sl < s.splits; sl++) v += glb(s.cs_part)[(b * s.splits + sl) * s.n + jn];
+            const int64_t b = s.batch == 1 ? 0 : c / s.n, jn = s.batch == 1 ? c : c % s.n;
+            const float v = sum_slices(glb(s.cs_part) + b * s.splits * s.n + jn, s.n, s.splits, 0.f);
             glb(s.cs_dst)[b * s.cs_stride + jn] += v;
         }
     }
