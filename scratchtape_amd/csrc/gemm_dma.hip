@@ -462,6 +462,20 @@ bool dma_plan(const st::DmaGemm &d, DmaPlan &p) {
         p.bn = cands[best].bn;
         p.slice_k = cdiv(cdiv(k, best_splits), BK) * BK;
         p.splits = cdiv(k, p.slice_k);
+        // Long-k products (a weight gradient Xᵀ·dY over T = 4,096 tokens):
+        // slices of at most 16 k-stages, the count doubled while fewer than
+        // 256 workgroups run.  Measured on MI355X (f16 route, as single calls):
+        // 256x4096x768 19.0 -> 16.0 us, 256x4096x1024 18.7 -> 18.3 us,
+        // 1024x4096x256 19.5 -> 18.6 us, 256x4096x256 unchanged at 16 slices;
+        // the same rule on k = 768..1,024 products (split 2) was 3-5 us slower.
+        if (can_split && k >= 2048) {
+            const int64_t tiles = batch * (m / p.bm) * (n / p.bn);
+            int64_t sp = 1;
+            while (k / sp > 16 * BK && k / (2 * sp) >= 4 * BK && sp < 64) sp *= 2;
+            while (tiles * sp < 256 && k / (2 * sp) >= 8 * BK) sp *= 2;
+            p.slice_k = cdiv(cdiv(k, sp), BK) * BK;
+            p.splits = cdiv(k, p.slice_k);
+        }
     }
     const int64_t dma_wgs = best >= 0 ? batch * (m / p.bm) * (n / p.bn) * p.splits : 0;
     p.tiny = tiny_ok && (best < 0 || (dma_wgs < 256 && tiny_wgs >= 2 * dma_wgs));
