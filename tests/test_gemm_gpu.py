@@ -141,6 +141,8 @@ DMA_CASES = [
     (1, 256, 2048, 128, False, False, False, False, True, True),
     (3, 64, 1024, 64, False, False, False, False, True, True),
     (1, 64, 4096, 64, False, False, False, False, False, True),
+    # 32 slices of 256 (long-k split rule): the split sum's loads go out in two blocks of 16
+    (1, 64, 8192, 64, False, False, False, False, True, True),
     # m, n multiples of 32 but not of 64: the f32 route's 32 x 32 tiles (the f16 route takes k_gemm)
     (1, 96, 256, 160, True, True, True, True, True, False),
     (2, 32, 1024, 96, False, False, False, False, True, True),
