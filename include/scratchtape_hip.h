@@ -126,7 +126,7 @@ typedef struct st_gemm {
 st_status st_matmul_grouped(const st_gemm *gemms, int64_t count, st_stream stream);
 
 /* Size of the fixed device scratch of st_matmul_grouped_noalloc. */
-#define ST_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define ST_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* No counterpart in the reference: st_matmul_grouped for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

@@ -35,7 +35,7 @@ pub const ST_ERR_OOM: st_status = -3;
 pub const ST_ERR_NO_DEVICE: st_status = -4;
 
 /// Size of the fixed device scratch of `st_matmul_grouped_noalloc`.
-pub const ST_NOALLOC_SCRATCH_BYTES: u32 = 32 << 20;
+pub const ST_NOALLOC_SCRATCH_BYTES: u32 = 64 << 20;
 
 /// `hipStream_t`; null is the default stream.
 pub type st_stream = *mut c_void;

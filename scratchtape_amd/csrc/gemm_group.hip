@@ -56,6 +56,12 @@ struct Cfg {
     static constexpr int LA = TM / (8 * WAVES), LB = TN / (8 * WAVES);  // DMA wave-loads per wave per stage
     static_assert(WM == 64 && WN == 64, "64 x 64 per wave");
     static_assert(NS * (SA + SB) * 4 <= 160 * 1024, "LDS");
+    // Split-k keeps a 256-row unit to half a CU's fair share of k-stages.
+    // Timed on the d_model-256 training step's 15 GEMMs (fair share 39
+    // stages), whose five dW GEMMs (k = 4096) the whole share cuts into 4
+    // slices of 32 stages: 8 slices of 16 take the call 211.5 -> 197.1 us;
+    // 16 slices of 8 220.9 us.
+    static constexpr double FAIR_PART = TM == 256 ? 0.5 : 1.0;
 };
 using Tall = Cfg<256, 4, 3>;
 using Square = Cfg<128, 2, 4>;
@@ -524,6 +530,10 @@ struct Cfg {
     static constexpr int SA = TM * 64, SB = TN * 64;    // bytes of a stage (f16)
     static constexpr int SLOT = SA + SB;
     static constexpr int NS = 5;                        // every unit (split slice) keeps NS - 1 = 4 stages
+    // Split-k keeps a unit to a CU's whole fair share of k-stages: finer
+    // slices of the d_model-256 step's dW GEMMs (8 instead of 4, 16 stages
+    // each) take that call 57.5 -> 67.5 us, the larger split-k sum included.
+    static constexpr double FAIR_PART = 1.0;
     // The kernel's LDS: NSL + 1 slots (the last for the unused conversion
     // past the final stage), their column-sum partials, the slot counters,
     // the group's arguments and their prefix sums.
@@ -1222,17 +1232,18 @@ void schedule(GroupArgs &ga, int L) {
 }
 
 // Split-k where the epilogue allows it, so that no unit holds more k-stages
-// than a CU's fair share of the whole group (nor fewer than 4); TM-row tiles,
-// every slice keeps at least NS - 1 stages.
-void group_splits(const st::DmaGemm *items, int count, int TM, int NS, int cus, std::vector<int64_t> &splits,
-                  std::vector<int64_t> &slice_k) {
+// than fair_part times a CU's fair share of the whole group (taken as at
+// least 8), and none fewer than 4; TM-row tiles, every slice keeps at least
+// NS - 1 stages.
+void group_splits(const st::DmaGemm *items, int count, int TM, int NS, double fair_part, int cus,
+                  std::vector<int64_t> &splits, std::vector<int64_t> &slice_k) {
     using st::DmaGemm;
     splits.assign(count, 1);
     slice_k.assign(count, 0);
     double total = 0;
     for (int i = 0; i < count; i++)
         total += (double)items[i].batch * (items[i].m / TM) * (items[i].n / TN) * (items[i].k / BK);
-    const double fair = std::max(8.0, total / cus);
+    const double fair = std::max(8.0, fair_part * total / cus);
     for (int i = 0; i < count; i++) {
         const DmaGemm &d = items[i];
         int64_t sp = 1;
@@ -1275,7 +1286,7 @@ st_status launch_group(const st::DmaGemm *items, int count, void (*kern)(GroupAr
     const int cus = group_cus();
 
     std::vector<int64_t> splits, slice_k;
-    group_splits(items, count, TM, NS, cus, splits, slice_k);
+    group_splits(items, count, TM, NS, C::FAIR_PART, cus, splits, slice_k);
     // Longest units first.
     std::vector<int> order(count);
     std::iota(order.begin(), order.end(), 0);
@@ -1416,8 +1427,9 @@ st_status check_group_waits() {
 
 size_t gemm_group_scratch(const DmaGemm *items, int count, bool f16, bool tall) {
     const int TM = tall ? 256 : 128, NS = f16 ? r16::Tall16::NS : (tall ? Tall::NS : Square::NS);
+    const double fair_part = f16 ? r16::Tall16::FAIR_PART : (tall ? Tall::FAIR_PART : Square::FAIR_PART);
     std::vector<int64_t> splits, slice_k;
-    group_splits(items, count, TM, NS, group_cus(), splits, slice_k);
+    group_splits(items, count, TM, NS, fair_part, group_cus(), splits, slice_k);
     return sizeof(float) * group_part_floats(items, count, splits);
 }
 

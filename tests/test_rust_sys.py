@@ -183,7 +183,7 @@ def test_constants_match_the_header():
     defines, consts = header_defines(), rust_consts()
     for name in ["ST_OK", "ST_ERR_INVALID", "ST_ERR_HIP", "ST_ERR_OOM", "ST_ERR_NO_DEVICE"]:
         assert int(consts[name]) == int(defines[name].strip("()")), name
-    c_bytes = eval(defines["ST_NOALLOC_SCRATCH_BYTES"].replace("u", ""))  # "(32u << 20)"
+    c_bytes = eval(defines["ST_NOALLOC_SCRATCH_BYTES"].replace("u", ""))  # "(64u << 20)"
     assert eval(consts["ST_NOALLOC_SCRATCH_BYTES"]) == c_bytes
 
 

@@ -49,8 +49,8 @@ def test_noalloc_matches_the_allocating_entry_point(dev, use_f16):
 
 def test_noalloc_refuses_partials_beyond_its_scratch(dev):
     """A group whose f32 split-k partials (with column sums) need more than ST_NOALLOC_SCRATCH_BYTES: a wide
-    GEMM makes the group use 256-row tiles, and a 256 x 131072 x 1024 GEMM with column sums then splits k 32 ways
-    (32 MiB of partials plus 128 KiB of column-sum partials)."""
+    GEMM makes the group use 256-row tiles, and a 256 x 131072 x 1024 GEMM with column sums then splits k 64 ways
+    (64 MiB of partials plus 256 KiB of column-sum partials)."""
     big_a, big_b, big_o = (torch.zeros(s, device=dev) for s in ((4096, 128), (128, 4096), (4096, 4096)))
     a = torch.zeros(256, 131072, device=dev)
     b = torch.zeros(131072, 1024, device=dev)
