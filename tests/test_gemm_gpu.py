@@ -6,6 +6,8 @@ Tolerances (scale-relative: max|gpu - cpu| / max|cpu|, as matmul.rs:1077-1086):
                        different summation order) and <= 2e-3 vs the f32 oracle
   column sums       <= 1e-4 (f32) / 1e-3 (f16) of their scale, as matmul.rs:1081
 """
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -367,6 +369,31 @@ def test_grouped_equals_single_calls_bit_for_bit_without_split(dev, use_f16):
         p["oh"].copy_(torch.from_numpy(p["out0"]).to(dev))
         st.matmul_with(*p["call"])
         np.testing.assert_array_equal(g, p["oh"].cpu().numpy(), err_msg=p["what"])
+
+
+def test_grouped_random_groups_match_oracle(dev):
+    # Seeded random groups of 1-5 GEMMs: both routes, tile-divisible and ragged shapes,
+    # batches, transposes, every epilogue term, packed outputs (split-k allowed) or not.
+    rnd = random.Random(11)
+    for gi in range(12):
+        use_f16 = gi % 2 == 1
+        ps = []
+        for i in range(rnd.randint(1, 5)):
+            if rnd.random() < 0.2:
+                m, k, n = rnd.randint(1, 160), rnd.randint(1, 300), rnd.randint(1, 160)
+            else:
+                m, n = rnd.choice([64, 128, 256, 384]), rnd.choice([64, 128, 256])
+                k = rnd.choice([32, 96, 256, 512, 1024, 2048])
+            batch = rnd.choice([1, 1, 2, 3])
+            while batch * m * n * k > (1 << 24) and k > 32:
+                k //= 2
+            epi = [rnd.random() < 0.3 for _ in range(5)]  # bias, relu, mask, residual, accumulate
+            case = (batch, m, k, n, rnd.random() < 0.5, rnd.random() < 0.5, *epi)
+            packed = not any(epi[:4]) and rnd.random() < 0.7
+            ps.append(prep_case(dev, 500 + 8 * gi + i, case, use_f16, aligned16=True, packed=packed))
+        st.matmul_grouped([p["call"] for p in ps])
+        for p in ps:
+            check_case(p)
 
 
 @pytest.mark.parametrize("use_f16", [False, True])
