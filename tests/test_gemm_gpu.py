@@ -371,26 +371,40 @@ def test_grouped_equals_single_calls_bit_for_bit_without_split(dev, use_f16):
         np.testing.assert_array_equal(g, p["oh"].cpu().numpy(), err_msg=p["what"])
 
 
+def random_case(rnd):
+    """A GEMM case (and whether its outputs are packed) drawn by rnd: tile-divisible or ragged
+    shapes, batches, transposes, every epilogue term; at most 2^24 multiply-adds."""
+    if rnd.random() < 0.2:
+        m, k, n = rnd.randint(1, 160), rnd.randint(1, 300), rnd.randint(1, 160)
+    else:
+        m, n = rnd.choice([64, 128, 256, 384]), rnd.choice([64, 128, 256])
+        k = rnd.choice([32, 96, 256, 512, 1024, 2048])
+    batch = rnd.choice([1, 1, 2, 3])
+    while batch * m * n * k > (1 << 24) and k > 32:
+        k //= 2
+    epi = [rnd.random() < 0.3 for _ in range(5)]  # bias, relu, mask, residual, accumulate
+    case = (batch, m, k, n, rnd.random() < 0.5, rnd.random() < 0.5, *epi)
+    return case, not any(epi[:4]) and rnd.random() < 0.7
+
+
+def test_random_single_calls_match_oracle(dev):
+    # Seeded random cases one call each: the dispatch's tile, split-k and small-product choices.
+    rnd = random.Random(12)
+    for ci in range(24):
+        case, packed = random_case(rnd)
+        p = prep_case(dev, 700 + ci, case, ci % 2 == 1, aligned16=True, packed=packed)
+        st.matmul_with(*p["call"])
+        check_case(p)
+
+
 def test_grouped_random_groups_match_oracle(dev):
-    # Seeded random groups of 1-5 GEMMs: both routes, tile-divisible and ragged shapes,
-    # batches, transposes, every epilogue term, packed outputs (split-k allowed) or not.
+    # Seeded random groups of 1-5 GEMMs on both routes, outputs packed (split-k allowed) or not.
     rnd = random.Random(11)
     for gi in range(12):
-        use_f16 = gi % 2 == 1
         ps = []
         for i in range(rnd.randint(1, 5)):
-            if rnd.random() < 0.2:
-                m, k, n = rnd.randint(1, 160), rnd.randint(1, 300), rnd.randint(1, 160)
-            else:
-                m, n = rnd.choice([64, 128, 256, 384]), rnd.choice([64, 128, 256])
-                k = rnd.choice([32, 96, 256, 512, 1024, 2048])
-            batch = rnd.choice([1, 1, 2, 3])
-            while batch * m * n * k > (1 << 24) and k > 32:
-                k //= 2
-            epi = [rnd.random() < 0.3 for _ in range(5)]  # bias, relu, mask, residual, accumulate
-            case = (batch, m, k, n, rnd.random() < 0.5, rnd.random() < 0.5, *epi)
-            packed = not any(epi[:4]) and rnd.random() < 0.7
-            ps.append(prep_case(dev, 500 + 8 * gi + i, case, use_f16, aligned16=True, packed=packed))
+            case, packed = random_case(rnd)
+            ps.append(prep_case(dev, 500 + 8 * gi + i, case, gi % 2 == 1, aligned16=True, packed=packed))
         st.matmul_grouped([p["call"] for p in ps])
         for p in ps:
             check_case(p)
