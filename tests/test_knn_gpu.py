@@ -145,6 +145,22 @@ def test_search_skips_probe_ids_outside_the_cells(dev):
 
 
 @pytest.mark.usefixtures("scan_order")
+def test_search_random_stores(dev):
+    # Seeded random stores (cells of up to 5, 100 or 3000 keys, empty ones included), query
+    # magnitudes 2^-20 .. 2^20, probe lists with repeats, nprobe 1..16 and several k.
+    rng = np.random.default_rng(47)
+    for _ in range(6):
+        ncells = int(rng.integers(1, 400))
+        sizes = rng.integers(0, int(rng.choice([5, 100, 3000])), ncells)
+        store, codes, scales, cs = make_store(dev, sizes, int(rng.integers(1 << 30)))
+        nq = int(rng.integers(1, 200))
+        nprobe = int(rng.integers(1, min(16, ncells) + 1))
+        queries = (rng.standard_normal((nq, D)) * np.exp2(rng.integers(-20, 21, (nq, 1)))).astype(np.float32)
+        probes = rng.integers(0, ncells, (nq, nprobe)).astype(np.int32)
+        check_search(dev, store, codes, scales, cs, queries, probes, int(rng.choice([1, 7, 64, 128])))
+
+
+@pytest.mark.usefixtures("scan_order")
 def test_search_many_queries_sharing_cells(dev):
     # 600 queries x 8 probes over 100 cells: every cell is probed by ~48 queries.
     rng = np.random.default_rng(31)
