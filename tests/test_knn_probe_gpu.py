@@ -130,3 +130,20 @@ def test_probe_selection_under_ties_and_round_edges(dev, case):
         assert list(got[0]) == list(range(16))
     if case == "one_cell_last_round":
         assert got[1, 0] == 12288
+
+
+def test_probe_random_indexes(dev):
+    # Seeded random indexes: 1..5000 cells, magnitudes 2^-25 .. 2^25 on both sides, duplicated
+    # centroids (ties to the lower id), zero queries, nprobe 1..16.
+    rng = np.random.default_rng(35)
+    for _ in range(8):
+        nlist = int(rng.choice([int(rng.integers(1, 100)), int(rng.integers(100, 5000))]))
+        nq = int(rng.integers(1, 300))
+        nprobe = int(rng.integers(1, min(16, nlist) + 1))
+        cent = (rng.standard_normal((nlist, D)) * np.exp2(rng.integers(-25, 26, (nlist, 1)))).astype(np.float32)
+        if rng.random() < 0.5:
+            cent[rng.integers(0, nlist, max(1, nlist // 10))] = cent[int(rng.integers(0, nlist))]
+        queries = (rng.standard_normal((nq, D)) * np.exp2(rng.integers(-25, 26, (nq, 1)))).astype(np.float32)
+        queries[0] = 0.0
+        _, got = run_probe(dev, cent, queries, nprobe)
+        np.testing.assert_array_equal(got, oracle.knn_probe(cent, queries, nprobe))
