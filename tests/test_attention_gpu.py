@@ -6,6 +6,8 @@ Tolerances (scale-relative): f32 route 1e-5 on P and O, 1e-4 on the gradients
 the oracle run on f16-rounded Q, K, V (the BJ attention contract).  Softmax
 kernels alone: forward 1e-5, backward 1e-4 (rows.rs:497-500).
 """
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -138,3 +140,10 @@ def test_fused_attention_agrees_with_the_unfused_f16_route(dev):
     torch.cuda.synchronize()
     assert rel_err(fb.ctx.cpu().numpy(), ub.ctx.cpu().numpy()) <= 2e-3
     assert rel_err(fb.dqkv.cpu().numpy(), ub.dqkv.cpu().numpy()) <= 4e-3
+
+
+def test_fused_attention_random_shapes(dev):
+    # Seeded random batches, head counts, every T = 32 .. 256 step 32 among them, softmax1 or not.
+    rnd = random.Random(23)
+    for i, t in enumerate(rnd.sample(range(32, 257, 32), 8)):
+        fused_case(dev, rnd.randint(1, 3), rnd.randint(1, 4), t, rnd.random() < 0.5, 300 + i)

@@ -3,6 +3,8 @@ the CPU tape; gpu_step/rows.rs:60-99, 177-293 on the device), as the reference's
 layer_norm_matches_cpu_tape (rows.rs:405-454) checks them: y within 1e-5, dx, dgamma
 and dbeta within 1e-4 (scale-relative), gamma/beta at an offset in a flat parameter
 buffer with nothing written outside, accumulate doubling dx."""
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -92,3 +94,14 @@ def test_layer_norm_back_to_back_shapes(dev):
     """Calls of different shapes back to back, each checked (the row scratch arena is reused across them)."""
     for nrows, d in [(4096, 256), (37, 24), (600, 520), (4096, 256)]:
         run_case(dev, nrows, d, 0, seed=nrows)
+
+
+def test_layer_norm_random_shapes(dev):
+    # Seeded random shapes: widths 1..1100 (vector and scalar forms), parameter offsets 0..8,
+    # one to three models, rows 1..700.
+    rnd = random.Random(19)
+    for i in range(10):
+        models = rnd.choice([1, 1, 2, 3])
+        nrows = models * rnd.randint(1, 700 // models)
+        d = rnd.choice([rnd.randint(1, 1100), 4 * rnd.randint(1, 256)])
+        run_case(dev, nrows, d, rnd.randint(0, 8), models, seed=40 + i)
