@@ -214,7 +214,7 @@ __device__ void locate(const GroupArgs &ga, const int32_t *cum, int x, int j, in
 
 // grid: a multiple of 8 workgroups, at most one per CU (the ring takes most
 // of the LDS).  Every GEMM's unit has at least NS - 1 k-stages.
-template <class C, bool F16>
+template <class C>
 __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
     constexpr int TM = C::TM, NS = C::NS, SA = C::SA, SB = C::SB, LA = C::LA, LB = C::LB;
     constexpr int WM = C::WM, WN = C::WN, FM = C::FM, FN = C::FN;
@@ -264,30 +264,16 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
 #pragma unroll
     for (int st = 0; st < NS - 1; st++) issue(cur);
 
-    // Accumulators: the f32 route's 16 x 16 blocks (v_mfma_f32_16x16x4_f32), or
-    // the f16 route's 32 x 32 blocks (v_mfma_f32_32x32x16_f16, which on gfx950
-    // does twice the work of v_mfma_f32_16x16x32_f16 in the same issue time).
-    constexpr int M32 = WM / 32, N32 = WN / 32;
-    f32x4 acc[FM][FN];
-    f32x16 acc2[M32][N32];
+    f32x4 acc[FM][FN];  // 16 x 16 blocks (v_mfma_f32_16x16x4_f32)
     while (true) {
         const GProb &g = sga.p[cur.p];
         const int gflags = uni(g.flags), gsplits = uni(g.splits);
         const bool do_cs = (gflags & F_CS) && cur.row0 == 0;
         float cs_acc = 0.f;  // column sum of B for column col0 + tid (tid < TN), this slice
-        if constexpr (F16) {
 #pragma unroll
-            for (int i = 0; i < M32; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int jn = 0; jn < N32; jn++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) acc2[i][jn][e] = 0.f;
-        } else {
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+            for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         // Stage st of cur: wait for this wave's DMA of it (younger stages,
         // possibly the next unit's, stay in flight), barrier (every wave's
@@ -310,52 +296,19 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
                 rslot = rslot + SLOT == NS * SLOT ? 0 : rslot + SLOT;
                 const float *lb = la + SA;
                 const int gq = lane >> 4;
-                if constexpr (F16) {
-                    // 32 x 32 x 16 operands: lane l holds row (or column) l % 32
-                    // and the 8 k of group 2 ks + l / 32 of the stage.
-                    half8 af[M32][2], bf[N32][2];
-                    const int r32 = lane & 31, h = lane >> 5;
+                // Lane group gq supplies k = 8 gq + u at MFMA step u, for A and B alike.
+                float ax[FM][8], bx8[FN][8];
 #pragma unroll
-                    for (int i = 0; i < M32; i++)
+                for (int i = 0; i < FM; i++) frag<TM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, ax[i]);
 #pragma unroll
-                        for (int ks = 0; ks < 2; ks++) {
-                            float v[8];
-                            frag<TM, AKC>(la, wm * WM + i * 32 + r32, 2 * ks + h, v);
+                for (int jn = 0; jn < FN; jn++) frag<TN, BKC>(lb, wn * WN + jn * 16 + (lane & 15), gq, bx8[jn]);
 #pragma unroll
-                            for (int e = 0; e < 8; e++) af[i][ks][e] = (_Float16)v[e];
-                        }
+                for (int u = 0; u < 8; u++)
 #pragma unroll
-                    for (int jn = 0; jn < N32; jn++)
+                    for (int i = 0; i < FM; i++)
 #pragma unroll
-                        for (int ks = 0; ks < 2; ks++) {
-                            float v[8];
-                            frag<TN, BKC>(lb, wn * WN + jn * 32 + r32, 2 * ks + h, v);
-#pragma unroll
-                            for (int e = 0; e < 8; e++) bf[jn][ks][e] = (_Float16)v[e];
-                        }
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                        for (int i = 0; i < M32; i++)
-#pragma unroll
-                            for (int jn = 0; jn < N32; jn++)
-                                acc2[i][jn] =
-                                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][ks], bf[jn][ks], acc2[i][jn], 0, 0, 0);
-                } else {
-                    float ax[FM][8], bx8[FN][8];
-#pragma unroll
-                    for (int i = 0; i < FM; i++) frag<TM, AKC>(la, wm * WM + i * 16 + (lane & 15), gq, ax[i]);
-#pragma unroll
-                    for (int jn = 0; jn < FN; jn++) frag<TN, BKC>(lb, wn * WN + jn * 16 + (lane & 15), gq, bx8[jn]);
-#pragma unroll
-                    for (int u = 0; u < 8; u++)
-#pragma unroll
-                        for (int i = 0; i < FM; i++)
-#pragma unroll
-                            for (int jn = 0; jn < FN; jn++)
-                                acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[i][u], bx8[jn][u], acc[i][jn], 0,
-                                                                                   0, 0);
-                }
+                        for (int jn = 0; jn < FN; jn++)
+                            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[i][u], bx8[jn][u], acc[i][jn], 0, 0, 0);
                 if (do_cs && tid < TN) {
                     float v[8];
 #pragma unroll
@@ -395,9 +348,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
         // mask <= 0, + residual, + out.
         bar();
         {
-            // Pitch: 16 banks between the 4-row groups of a 16 x 16 block, 32
-            // between the two lane halves of a 32 x 32 block.
-            constexpr int EP = F16 ? WN + 8 : WN + 4;
+            // Pitch: 16 banks between the 4-row groups of a 16 x 16 block.
+            constexpr int EP = WN + 4;
             float *ep = lds + (rslot == 0 ? NS * SLOT : rslot) / 4 - (SA + SB) + wave * 16 * EP;
             const bool split = gsplits > 1;
             float *const P = split ? g.out + (cur.zb * gsplits + cur.slice) * (int64_t)g.m * g.n : nullptr;
@@ -407,22 +359,11 @@ __global__ __launch_bounds__(C::THREADS) void k_gemm_group(GroupArgs ga) {
             const gptr<const float> bias = glb(uni(g.bias)), mask = glb(uni(g.mask)), res = glb(uni(g.res));
 #pragma unroll
             for (int i = 0; i < FM; i++) {
-                if constexpr (F16) {
-                    // Rows 16 (i % 2) .. + 15 of 32 x 32 block i / 2: element e
-                    // of a lane is row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
 #pragma unroll
-                    for (int jn = 0; jn < N32; jn++)
+                for (int jn = 0; jn < FN; jn++)
 #pragma unroll
-                        for (int e = 0; e < 8; e++)
-                            ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * EP + jn * 32 + (lane & 31)] =
-                                acc2[i >> 1][jn][8 * (i & 1) + e];
-                } else {
-#pragma unroll
-                    for (int jn = 0; jn < FN; jn++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            ep[(4 * (lane >> 4) + r) * EP + jn * 16 + (lane & 15)] = acc[i][jn][r];
-                }
+                    for (int r = 0; r < 4; r++)
+                        ep[(4 * (lane >> 4) + r) * EP + jn * 16 + (lane & 15)] = acc[i][jn][r];
 #pragma unroll
                 for (int q = 0; q < 16 * WN / 4 / 64; q++) {
                     const int e = q * 64 + lane, row = e / (WN / 4), c4 = (e % (WN / 4)) * 4;
@@ -1437,8 +1378,8 @@ st_status gemm_group(const DmaGemm *items, int count, bool f16, bool tall, hipSt
     if (f16)
         return tall ? launch_group<r16::Tall16>(items, count, &r16::k_gemm_group16<r16::Tall16>, stream)
                     : launch_group<r16::Square16>(items, count, &r16::k_gemm_group16<r16::Square16>, stream);
-    return tall ? launch_group<Tall>(items, count, &k_gemm_group<Tall, false>, stream)
-                : launch_group<Square>(items, count, &k_gemm_group<Square, false>, stream);
+    return tall ? launch_group<Tall>(items, count, &k_gemm_group<Tall>, stream)
+                : launch_group<Square>(items, count, &k_gemm_group<Square>, stream);
 }
 
 }  // namespace st
